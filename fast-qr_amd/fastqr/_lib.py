@@ -1,0 +1,126 @@
+"""Loader for the gfx950 C-ABI library (libfastqr.so) and its CPython binding.
+
+The product path has no CPU or torch fallback: if the native library is
+missing or fails to load, every entry point raises ``FastQRUnavailable``.
+"""
+from __future__ import annotations
+
+import ctypes
+import importlib.util
+import os
+import sys
+from pathlib import Path
+
+PKG_DIR = Path(__file__).resolve().parent
+LIB_PATH = PKG_DIR / "libfastqr.so"
+EXT_PATH = PKG_DIR / "_fastqr_py.so"
+
+# status codes, include/fastqr.h
+FASTQR_OK = 0
+FASTQR_EINVAL = -1
+FASTQR_EWORKSPACE = -2
+FASTQR_ELAYOUT = -3
+FASTQR_EOVERLAP = -4
+FASTQR_ETESTHOOK = -99
+
+# every symbol include/fastqr.h declares
+EXPORTED_SYMBOLS = (
+    "fastqr_geqrf_f32",
+    "fastqr_workspace_bytes",
+    "fastqr_path_name",
+    "fastqr_last_error",
+    "fastqr_version",
+    "fastqr_debug_force_error",
+)
+
+
+class FastQRUnavailable(RuntimeError):
+    """The native library is not built or cannot be loaded."""
+
+
+class FastQRError(RuntimeError):
+    """A non-zero status from fastqr_geqrf_f32."""
+
+    def __init__(self, code: int, message: str):
+        super().__init__(f"fastqr error {code}: {message}")
+        self.code = code
+        self.message = message
+
+
+_cdll = None
+_ext = None
+
+
+def cdll() -> ctypes.CDLL:
+    """ctypes view of libfastqr.so with argtypes for every exported symbol."""
+    global _cdll
+    if _cdll is None:
+        if not LIB_PATH.exists():
+            raise FastQRUnavailable(
+                f"{LIB_PATH} is not built; run `make -C {PKG_DIR.parent}` or __graft_entry__.build()"
+            )
+        try:
+            lib = ctypes.CDLL(str(LIB_PATH))
+        except OSError as exc:  # pragma: no cover - depends on the host
+            raise FastQRUnavailable(f"cannot load {LIB_PATH}: {exc}") from exc
+        i64, vp, sz = ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t
+        lib.fastqr_geqrf_f32.argtypes = [vp, i64, i64, i64, i64, i64, vp, i64, i64, i64, vp, i64, i64, vp, sz, vp]
+        lib.fastqr_geqrf_f32.restype = ctypes.c_int
+        lib.fastqr_workspace_bytes.argtypes = [i64, i64]
+        lib.fastqr_workspace_bytes.restype = sz
+        lib.fastqr_path_name.argtypes = [i64]
+        lib.fastqr_path_name.restype = ctypes.c_char_p
+        lib.fastqr_last_error.argtypes = []
+        lib.fastqr_last_error.restype = ctypes.c_char_p
+        lib.fastqr_version.argtypes = []
+        lib.fastqr_version.restype = ctypes.c_int
+        lib.fastqr_debug_force_error.argtypes = [ctypes.c_int]
+        lib.fastqr_debug_force_error.restype = None
+        _cdll = lib
+    return _cdll
+
+
+def ext():
+    """The CPython binding module (_fastqr_py), loaded from this directory."""
+    global _ext
+    if _ext is None:
+        if not EXT_PATH.exists():
+            raise FastQRUnavailable(f"{EXT_PATH} is not built; run `make -C {PKG_DIR.parent}`")
+        cdll()  # load libfastqr.so first so the binding resolves against this copy
+        spec = importlib.util.spec_from_file_location("fastqr._fastqr_py", EXT_PATH)
+        if spec is None or spec.loader is None:  # pragma: no cover
+            raise FastQRUnavailable(f"cannot import {EXT_PATH}")
+        mod = importlib.util.module_from_spec(spec)
+        try:
+            spec.loader.exec_module(mod)
+        except ImportError as exc:  # pragma: no cover
+            raise FastQRUnavailable(f"cannot import {EXT_PATH}: {exc}") from exc
+        sys.modules.setdefault("fastqr._fastqr_py", mod)
+        _ext = mod
+    return _ext
+
+
+def loaded_paths() -> list[str]:
+    """Shared objects of this package currently mapped into the process."""
+    out = []
+    try:
+        with open("/proc/self/maps") as fh:
+            for line in fh:
+                if str(PKG_DIR) in line and line.rstrip().endswith(".so"):
+                    p = line.split()[-1]
+                    if p not in out:
+                        out.append(p)
+    except OSError:  # pragma: no cover
+        pass
+    return out
+
+
+def is_built() -> bool:
+    return LIB_PATH.exists() and EXT_PATH.exists()
+
+
+def env_flag(name: str, default: bool) -> bool:
+    raw = os.environ.get(name)
+    if raw is None or raw.strip() == "":
+        return default
+    return raw.strip().lower() not in {"0", "false", "no", "off"}

@@ -1,0 +1,108 @@
+/*
+ * fastqr.h — C ABI of the MI355X (gfx950) batched fp32 Householder QR.
+ *
+ * Drop-in native boundary for the reference's submission entrypoint
+ * `custom_kernel(data) -> (H, tau)` (official/submission.py:5-6,
+ * official/task.py:4-5).  The reference binds its kernels through pybind
+ * functions built with torch.utils.cpp_extension.load_inline; this header is
+ * the torch-free replacement for those bindings: plain pointers, int64 element
+ * strides and a HIP stream.  No function throws; every function returns a
+ * status code and records a message for fastqr_last_error().
+ *
+ * Output convention (LAPACK geqrf, as torch.geqrf): R in the upper triangle of
+ * H (diagonal included), Householder vectors v_k below the diagonal with the
+ * implicit v_k[k] = 1, and tau[k] such that H_k = I - tau[k] v_k v_k^T and
+ * A = H_0 H_1 ... H_{n-1} R.  Reflector sign convention as LAPACK slarfg:
+ * beta = -sign(alpha) * ||(alpha, x)||, tau = (beta - alpha) / beta, and
+ * tau = 0 (H column left as is) when x == 0.
+ */
+#ifndef FASTQR_H_
+#define FASTQR_H_
+
+#include <stddef.h>
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* Status codes.  Positive values are hipError_t codes from a failed launch. */
+#define FASTQR_OK 0
+#define FASTQR_EINVAL (-1)      /* bad shape, stride, or null pointer        */
+#define FASTQR_EWORKSPACE (-2)  /* workspace missing, misaligned or too small */
+#define FASTQR_ELAYOUT (-3)     /* H/tau layout not supported by the path     */
+#define FASTQR_EOVERLAP (-4)    /* A and H overlap with different layouts     */
+#define FASTQR_ETESTHOOK (-99)  /* error forced by fastqr_debug_force_error   */
+
+/*
+ * Batched QR of `batch` square n x n fp32 matrices.
+ *
+ * Replaces the reference's pybind entry points
+ *   geqrf32(data, h, tau)                        submissions/candidate.py:111-124
+ *   geqrf176(data, h, tau)                       submissions/candidate.py:251-270
+ *   geqrf352(data, h, tau)                       submissions/candidate.py:508-527
+ *   geqrf{n}_blocked(data, h, tau, n, false)     submissions/candidate.py:1333-1353
+ * with one shape-dispatched entry point (full factorisation only: the
+ * reference's factor_cols / project_tail arguments selected data-dependent
+ * shortcuts, which are not offered).
+ *
+ * A      device pointer, element (b, i, j) at A[b*a_s0 + i*a_s1 + j*a_s2]
+ *        (any strides, read only; as the reference kernels,
+ *        submissions/candidate.py:150-158).
+ * H      device pointer, element (b, i, j) at H[b*h_s0 + i*h_s1 + j*h_s2].
+ *        Columns must be contiguous (h_s1 == 1, h_s2 >= n); the allocator
+ *        layout is column-major (h_s0, h_s1, h_s2) = (n*n, 1, n) as
+ *        allocate_column_major_H (submissions/candidate.py:3752-3769).
+ *        H may be the same buffer as A only with an identical layout.
+ * tau    device pointer, element (b, k) at tau[b*tau_s0 + k*tau_s1].
+ * workspace / workspace_bytes   device scratch of at least
+ *        fastqr_workspace_bytes(batch, n) bytes, 256-byte aligned; may be
+ *        NULL when that size is 0.  It holds the per-panel T factors.
+ * stream a hipStream_t (0 = the null stream).  All work is enqueued
+ *        asynchronously on it; no host synchronisation.
+ *
+ * Returns FASTQR_OK, a negative FASTQR_E* argument error (nothing launched),
+ * or a positive hipError_t if a launch failed.
+ */
+int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n,
+                     int64_t a_s0, int64_t a_s1, int64_t a_s2,
+                     float* H, int64_t h_s0, int64_t h_s1, int64_t h_s2,
+                     float* tau, int64_t tau_s0, int64_t tau_s1,
+                     void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/*
+ * Workspace bytes fastqr_geqrf_f32 needs for (batch, n).  Replaces the
+ * reference's per-input cached policy/workspace tensors
+ * (allocate_h_tau / allocate_blocked_policy_workspace,
+ * submissions/candidate.py:3801-3880); only the T-factor scratch remains.
+ */
+size_t fastqr_workspace_bytes(int64_t batch, int64_t n);
+
+/*
+ * Name of the kernel path fastqr_geqrf_f32 takes for size n ("wave64",
+ * "lds", "blocked"); the reference's shape switch is custom_kernel
+ * (submissions/candidate.py:8383-8415).  Never NULL.
+ */
+const char* fastqr_path_name(int64_t n);
+
+/* Message for the last non-zero status on the calling thread (static storage,
+ * "" when none).  Replaces TORCH_CHECK / C10_CUDA_KERNEL_LAUNCH_CHECK text
+ * (submissions/candidate.py:112-122, 246). */
+const char* fastqr_last_error(void);
+
+/* ABI version of this header; bumped on any signature change. */
+int fastqr_version(void);
+
+/*
+ * Test hook: when `code` is non-zero the next fastqr_geqrf_f32 call on this
+ * thread returns `code` without launching anything (used to test the host's
+ * error path without faulting a GPU).  No counterpart in the reference.
+ */
+void fastqr_debug_force_error(int code);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FASTQR_H_ */

@@ -1,0 +1,145 @@
+"""GPU parity: the HIP path against the oracle (CPU torch.geqrf, the reference's
+own path: official/reference.py:145-147) on identical seeded fp32 inputs.
+
+Gates (oracle/checker.py):
+  * the reference evaluator's checker, official/reference.py:182-266;
+  * ||QR-A||_F/||A||_F <= 1e-5 n and ||Q^T Q - I||_F <= 1e-5 n;
+  * |R_ii| and tau within 1e-4 relative of CPU geqrf, same sign of R_ii, on
+    the columns above the rounding floor 4 sqrt(n) eps32 ||A||_2 / 1e-4.
+"""
+import sys
+
+import pytest
+import torch
+
+from fastqr import custom_kernel, inputs
+from oracle import checker
+
+pytestmark = pytest.mark.gpu
+
+
+def _say(msg):
+    print(msg, flush=True)
+    sys.stdout.flush()
+
+
+def run_gpu(a_cpu, dev):
+    a = a_cpu.to(dev)
+    h, tau = custom_kernel(a)
+    torch.cuda.synchronize()
+    return h.cpu(), tau.cpu()
+
+
+def assert_parity(a_cpu, h, tau, agree=True):
+    ok, msg = checker.official_check(a_cpu, h, tau)
+    assert ok, msg
+    rep = checker.frobenius_gates(a_cpu, h, tau)
+    assert rep.ok, rep.message()
+    if agree:
+        h_ref, tau_ref = torch.geqrf(a_cpu)
+        ag = checker.rdiag_tau_agreement(a_cpu, h, tau, h_ref, tau_ref)
+        assert ag.ok, ag.message()
+        return ag
+    return None
+
+
+def gaussian(batch, n, seed):
+    g = torch.Generator().manual_seed(seed)
+    return torch.randn((batch, n, n), generator=g, dtype=torch.float32)
+
+
+@pytest.mark.parametrize("n", [1, 2, 3, 5, 8, 15, 16, 17, 31, 32, 33, 48, 63, 64])
+def test_wave_path_matches_geqrf(cuda, n):
+    _say(f"[wave] n={n}")
+    a = gaussian(7, n, 100 + n)
+    h, tau = run_gpu(a, cuda)
+    assert h.stride() == (n * n, 1, n)
+    assert_parity(a, h, tau)
+
+
+@pytest.mark.parametrize("n", [65, 96, 100, 127, 128, 176, 200, 256, 352])
+def test_blocked_path_matches_geqrf(cuda, n):
+    _say(f"[blocked] n={n}")
+    a = gaussian(5, n, 200 + n)
+    h, tau = run_gpu(a, cuda)
+    assert h.stride() == (n * n, 1, n)
+    assert_parity(a, h, tau)
+
+
+@pytest.mark.parametrize("n", [32, 176, 512])
+def test_upper_triangular_input_is_left_unchanged(cuda, n):
+    # known answer from the reference's tests (tests/test_qr_smoke.py:8078-8085):
+    # an exactly upper-triangular input needs no reflection, tau == 0 and H == A.
+    _say(f"[upper] n={n}")
+    a = torch.triu(gaussian(3, n, 300 + n)) + torch.eye(n)
+    h, tau = run_gpu(a, cuda)
+    assert torch.equal(tau, torch.zeros_like(tau))
+    assert torch.equal(h, a)
+
+
+@pytest.mark.parametrize("n", [8, 100])
+def test_zero_matrix(cuda, n):
+    _say(f"[zero] n={n}")
+    a = torch.zeros((2, n, n))
+    h, tau = run_gpu(a, cuda)
+    assert torch.equal(tau, torch.zeros_like(tau))
+    assert torch.equal(h, a)
+
+
+@pytest.mark.parametrize("n", [32, 176])
+def test_column_major_and_strided_inputs(cuda, n):
+    _say(f"[strides] n={n}")
+    a = gaussian(4, n, 400 + n)
+    h_ref, tau_ref = run_gpu(a, cuda)
+    a_cm = a.transpose(1, 2).contiguous().transpose(1, 2)  # column-major view, same values
+    h2, tau2 = run_gpu(a_cm, cuda)
+    assert torch.equal(h2, h_ref) and torch.equal(tau2, tau_ref)
+    big = torch.zeros((8, n + 3, n + 5))
+    big[::2, 1 : n + 1, 2 : n + 2] = a
+    view = big.to(cuda)[::2, 1 : n + 1, 2 : n + 2]
+    h3, tau3 = custom_kernel(view)
+    torch.cuda.synchronize()
+    assert torch.equal(h3.cpu(), h_ref) and torch.equal(tau3.cpu(), tau_ref)
+
+
+def test_deterministic_rerun_is_bitwise_identical(cuda):
+    _say("[determinism]")
+    a = gaussian(6, 352, 5)
+    d = a.to(cuda)
+    h1, t1 = custom_kernel(d)
+    h1, t1 = h1.clone(), t1.clone()
+    h2, t2 = custom_kernel(d)
+    torch.cuda.synchronize()
+    assert torch.equal(h1, h2) and torch.equal(t1, t2)
+
+
+def test_input_is_not_written(cuda):
+    _say("[readonly]")
+    a = gaussian(3, 128, 6).to(cuda)
+    before = a.clone()
+    custom_kernel(a)
+    torch.cuda.synchronize()
+    assert torch.equal(a, before)
+
+
+WORKLOAD_CASES = [
+    ("C1", 0, None),
+    ("C2", 0, None),
+    ("C2", 1, None),
+    ("C3", 0, 24),
+    ("C4", 0, 8),
+    ("C5", 0, 2),
+    ("C5", 1, 1),
+]
+
+
+@pytest.mark.parametrize("name,idx,limit", WORKLOAD_CASES)
+def test_benchmark_workloads_match_geqrf(cuda, name, idx, limit):
+    shape = inputs.WORKLOADS[name][idx]
+    _say(f"[workload] {name} {shape.label} first {limit or shape.batch}")
+    a = inputs.generate(shape)
+    if limit is not None:
+        a = a[:limit].contiguous()
+    h, tau = run_gpu(a, cuda)
+    ag = assert_parity(a, h, tau)
+    _say(f"  {ag.message()}")
