@@ -1,0 +1,318 @@
+#!/usr/bin/env python3
+"""bench.py — batched fp32 Householder QR on one MI355X.
+
+Metric (the reference's ranking rule, official/task.yml:68-69,81): geometric
+mean of microseconds per custom_kernel call over the five benchmark workloads
+(C2 and C5 hold two shapes each and count as the geomean of their two shapes):
+
+  C1  20 x 32         N(0,1)
+  C2  40 x 176, 40 x 352   N(0,1)
+  C3  640 x 512       50% N(0,1), 25% rank-deficient, 25% clustered spectrum
+  C4  60 x 1024       75% N(0,1), 25% near-rank-deficient
+  C5  8 x 2048, 2 x 4096   N(0,1)
+
+Timing follows official/eval.py:157-222: per shape, `count` distinct inputs
+(count = clamp(256 MiB / input bytes, 1, 50), seed += 42 per input), a cache
+flush before every repeat (1 GiB here, as MI355X has a 256 MB Infinity Cache),
+HIP events around the `count` calls on torch's current stream, and a recheck
+of the outputs after the timed region.  One step = one such repeat of every
+shape.  A second, instrumented pass records per-kernel HIP events inside the
+library (fastqr_profile_*) to give each kernel's average launch duration and
+its roofline fraction.  CPU torch.geqrf (the reference's own path) is timed
+on this host's cores on a bounded sample of each shape.
+
+Prints ONE JSON line on stdout; human-readable lines go to stderr.
+"""
+from __future__ import annotations
+
+import argparse
+import json
+import math
+import os
+import statistics
+import sys
+import time
+from pathlib import Path
+
+ROOT = Path(__file__).resolve().parent
+for _p in (str(ROOT), str(ROOT / "fast-qr_amd")):
+    if _p not in sys.path:
+        sys.path.insert(0, _p)
+
+METRIC = "geomean µs/call over 5 configs; GFLOP/s (4n³/3) and % fp32 peak per shape"
+PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 (vector and MFMA)
+PEAK_HBM_GBS = 8000.0
+FLUSH_BYTES = 1 << 30
+INPUT_BYTES_TARGET = 256 * 1024 * 1024
+MAX_COUNT = 50
+
+
+def log(*a):
+    print(*a, file=sys.stderr, flush=True)
+
+
+def parse_args():
+    p = argparse.ArgumentParser(description=__doc__.split("\n")[0])
+    p.add_argument("--gpus", type=int, default=1)
+    p.add_argument("--steps", type=int, default=10)
+    p.add_argument("--warmup", type=int, default=2)
+    p.add_argument("--configs", default="C1,C2,C3,C4,C5", help="subset of workloads (headline needs all five)")
+    p.add_argument("--cpu-sample-seconds", type=float, default=3.0,
+                   help="target CPU seconds per shape for the torch.geqrf baseline (0 disables)")
+    p.add_argument("--no-check", action="store_true", help="skip the post-timing recheck")
+    p.add_argument("--no-profile", action="store_true", help="skip the instrumented per-kernel pass")
+    return p.parse_args()
+
+
+def count_for(batch: int, n: int) -> int:
+    per_input = 4 * batch * n * n
+    return max(1, min(MAX_COUNT, INPUT_BYTES_TARGET // per_input))
+
+
+def geomean(xs):
+    xs = [x for x in xs if x > 0]
+    return math.exp(sum(math.log(x) for x in xs) / len(xs)) if xs else float("nan")
+
+
+def main() -> int:
+    args = parse_args()
+    world = int(os.environ.get("WORLD_SIZE", "1"))
+    if args.gpus != 1 or world > 1:
+        log("bench.py measures one GPU only: every matrix is independent, so the path shards by batch "
+            "with no communication (see DESIGN.md); run with --gpus 1.")
+        return 2
+
+    import torch
+
+    import fastqr
+    from fastqr import _lib, inputs
+    from oracle import checker
+
+    if not torch.cuda.is_available():
+        log("no GPU visible")
+        return 1
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    ncores = len(os.sched_getaffinity(0))
+    torch.set_num_threads(ncores)
+    fastqr.ext()  # fail loudly if the native library is missing
+
+    names = [c.strip() for c in args.configs.split(",") if c.strip()]
+    shapes = [(name, s) for name in names for s in inputs.WORKLOADS[name]]
+
+    # ---- inputs -----------------------------------------------------------
+    data = {}
+    t0 = time.time()
+    for name, s in shapes:
+        cnt = count_for(s.batch, s.n)
+        lst = []
+        for i in range(cnt):
+            a = inputs.generate(s, seed=s.seed + 42 * (i + 1))
+            lst.append(a.to(dev))
+        data[s.label] = lst
+        log(f"[inputs] {name} {s.label}: {cnt} x {tuple(lst[0].shape)}")
+    log(f"[inputs] generated in {time.time() - t0:.1f}s")
+    flush_buf = torch.empty(FLUSH_BYTES // 8, dtype=torch.int64, device=dev)
+
+    def run_shape(label):
+        return [fastqr.custom_kernel(d) for d in data[label]]
+
+    # ---- warmup ------------------------------------------------------------
+    for _ in range(max(0, args.warmup)):
+        for _, s in shapes:
+            run_shape(s.label)
+    torch.cuda.synchronize()
+
+    # ---- timed region ---------------------------------------------------------
+    per_shape_us = {s.label: [] for _, s in shapes}
+    events = []
+    torch.cuda.synchronize()
+    wall0 = time.perf_counter()
+    for _ in range(args.steps):
+        for _, s in shapes:
+            flush_buf.fill_(42)
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            outs = run_shape(s.label)
+            e1.record()
+            events.append((s.label, e0, e1, len(outs)))
+    torch.cuda.synchronize()
+    wall = time.perf_counter() - wall0
+    for label, e0, e1, cnt in events:
+        per_shape_us[label].append(e0.elapsed_time(e1) * 1e3 / cnt)
+
+    # ---- recheck (last timed outputs of every shape) ---------------------------
+    checks = {}
+    if not args.no_check:
+        for _, s in shapes:
+            a_dev = data[s.label][-1]
+            h, tau = fastqr.custom_kernel(a_dev)
+            torch.cuda.synchronize()
+            k = min(s.batch, 4 if s.n <= 1024 else 1)
+            a_c, h_c, t_c = a_dev[:k].cpu(), h[:k].cpu(), tau[:k].cpu()
+            ok, msg = checker.official_check(a_c, h_c, t_c)
+            fro = checker.frobenius_gates(a_c, h_c, t_c)
+            checks[s.label] = bool(ok and fro.ok)
+            log(f"[check] {s.label}: official={'pass' if ok else 'FAIL'} {fro.message()}")
+            if not (ok and fro.ok):
+                log(f"[check] {s.label} FAILED: {msg}")
+
+    # ---- instrumented pass: per-kernel HIP events inside the library -----------
+    kernels = {}
+    if not args.no_profile:
+        for _, s in shapes:
+            _lib.profile_enable(True)
+            for _ in range(max(1, args.steps)):
+                run_shape(s.label)
+            torch.cuda.synchronize()
+            kernels[s.label] = _lib.profile_collect()
+            _lib.profile_enable(False)
+
+    # ---- CPU baseline: torch.geqrf on this host's cores ------------------------
+    cpu = {}
+    if args.cpu_sample_seconds > 0:
+        for _, s in shapes:
+            a_full = data[s.label][0]
+            # size the sample from a one-matrix probe
+            probe = a_full[:1].cpu()
+            t = time.perf_counter()
+            torch.geqrf(probe)
+            one = max(time.perf_counter() - t, 1e-6)
+            k = int(max(1, min(s.batch, args.cpu_sample_seconds / (3 * one))))
+            sample = a_full[:k].cpu().contiguous()
+            torch.geqrf(sample)  # warm
+            reps = []
+            for _ in range(3):
+                t = time.perf_counter_ns()
+                torch.geqrf(sample)
+                reps.append((time.perf_counter_ns() - t) / 1e3)
+            us_full = statistics.median(reps) * s.batch / k
+            cpu[s.label] = {"us_per_call": us_full, "sample_batch": k}
+            log(f"[cpu] {s.label}: torch.geqrf {us_full:.1f} us/call (sample {k}/{s.batch}, {ncores} threads)")
+
+    # ---- report ---------------------------------------------------------------------
+    shape_rows = {}
+    cfg_us = {}
+    cfg_cpu = {}
+    for name in names:
+        us_list, cpu_list = [], []
+        for s in inputs.WORKLOADS[name]:
+            us = statistics.median(per_shape_us[s.label])
+            best = min(per_shape_us[s.label])
+            fl = inputs.flops(s.batch, s.n)
+            row = {
+                "batch": s.batch,
+                "n": s.n,
+                "us_per_call": round(us, 3),
+                "best_us": round(best, 3),
+                "matrices_per_s": round(s.batch / (us * 1e-6), 1),
+                "gflops": round(fl / (us * 1e-6) / 1e9, 2),
+                "pct_fp32_peak": round(100.0 * fl / (us * 1e-6) / (PEAK_FP32_TFLOPS * 1e12), 2),
+                "hbm_gbs_algorithmic": round(inputs.bytes_moved(s.batch, s.n) / (us * 1e-6) / 1e9, 1),
+                "path": fastqr.path_for(s.n),
+            }
+            if s.label in checks:
+                row["check"] = "pass" if checks[s.label] else "FAIL"
+            if s.label in kernels:
+                kk = {}
+                for kname, st in kernels[s.label].items():
+                    if st["launches"] == 0:
+                        continue
+                    ms = st["ms"]
+                    kk[kname] = {
+                        "launches": st["launches"],
+                        "avg_us": round(ms * 1e3 / st["launches"], 3),
+                        "share": None,
+                        "tflops": round(st["flops"] / (ms * 1e-3) / 1e12, 2) if ms > 0 else None,
+                        "gbs": round(st["bytes"] / (ms * 1e-3) / 1e9, 1) if ms > 0 else None,
+                    }
+                tot_ms = sum(st["ms"] for st in kernels[s.label].values())
+                for kname in kk:
+                    kk[kname]["share"] = round(kernels[s.label][kname]["ms"] / tot_ms, 3) if tot_ms else None
+                if "update" in kk and kk["update"]["tflops"] is not None:
+                    kk["update"]["pct_fp32_mfma_peak"] = round(100 * kk["update"]["tflops"] / PEAK_FP32_TFLOPS, 2)
+                row["kernels"] = kk
+            if s.label in cpu:
+                row["cpu_geqrf_us"] = round(cpu[s.label]["us_per_call"], 1)
+                row["speedup_vs_cpu"] = round(cpu[s.label]["us_per_call"] / us, 1)
+                cpu_list.append(cpu[s.label]["us_per_call"])
+            shape_rows[s.label] = row
+            us_list.append(us)
+            log(f"[gpu] {name} {s.label}: {us:9.1f} us/call  {row['gflops']:9.1f} GFLOP/s  "
+                f"{row['pct_fp32_peak']:5.2f}% fp32 peak  path={row['path']}")
+        cfg_us[name] = geomean(us_list)
+        if cpu_list:
+            cfg_cpu[name] = geomean(cpu_list)
+
+    value = geomean(list(cfg_us.values()))
+    cpu_value = geomean(list(cfg_cpu.values())) if cfg_cpu else None
+
+    # roofline of the dominant kernel (the fp32-MFMA trailing update) over the workload
+    roof = None
+    if kernels:
+        agg = {"launches": 0, "ms": 0.0, "flops": 0.0, "bytes": 0.0}
+        per_kind_ms = {}
+        for label, kd in kernels.items():
+            for kname, st in kd.items():
+                per_kind_ms[kname] = per_kind_ms.get(kname, 0.0) + st["ms"]
+            st = kd["update"]
+            for f in agg:
+                agg[f] += st[f]
+        if agg["launches"] and agg["ms"] > 0:
+            avg_s = agg["ms"] * 1e-3 / agg["launches"]
+            achieved = agg["flops"] / agg["launches"] / avg_s / 1e12
+            roof = {
+                "bound": "mfma",
+                "kernel": "update_kernel (A2 -= V T^T V^T A2, v_mfma_f32_32x32x2f32)",
+                "achieved": round(achieved, 2),
+                "peak": PEAK_FP32_TFLOPS,
+                "unit": "TFLOP/s",
+                "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
+                "traffic": None,
+                "launches": agg["launches"],
+                "avg_launch_us": round(avg_s * 1e6, 3),
+                "flops_per_launch": agg["flops"] / agg["launches"],
+                "time_share_by_kernel": {k: round(v / sum(per_kind_ms.values()), 3) for k, v in per_kind_ms.items()
+                                         if v > 0},
+            }
+
+    line = {
+        "metric": METRIC,
+        "value": round(value, 3),
+        "unit": "us/call (geomean over configs)",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(wall * 1e3 / max(1, args.steps), 3),
+        "higher_is_better": False,
+        "scaling": "strong",
+        "vs_baseline": None,
+        "dtype": "f32",
+        "data": "synthetic: seeded N(0,1) and U diag(s) V^T (Haar U, V) families, generated on the CPU",
+        "config": {
+            "workload": "batched fp32 geqrf, configs " + ",".join(names) + " (C2, C5 = geomean of two shapes)",
+            "config_us": {k: round(v, 3) for k, v in cfg_us.items()},
+            "geomean_shapes_us": round(geomean([r["us_per_call"] for r in shape_rows.values()]), 3),
+            "shapes": shape_rows,
+        },
+        "roofline": roof,
+        "cpu_baseline": None if cpu_value is None else {
+            "value": round(cpu_value, 1),
+            "unit": "us/call (geomean over configs)",
+            "cores": torch.get_num_threads(),
+            "kind": "reference",
+            "sample": "torch.geqrf on CPU (the reference's ref_kernel / baseline_geqrf.py, MKL LAPACK) on the "
+                      "first input of each shape, a leading sub-batch sized to ~%.0fs per shape, median of 3 "
+                      "after 1 warm-up, scaled to the full batch" % args.cpu_sample_seconds,
+            "config_us": {k: round(v, 1) for k, v in cfg_cpu.items()},
+        },
+    }
+    print(json.dumps(line), flush=True)
+    if checks and not all(checks.values()):
+        return 3
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main())

@@ -10,6 +10,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <vector>
+
 #include "../../include/fastqr.h"
 #include "kernels.hpp"
 
@@ -44,9 +46,100 @@ int64_t span_elems(int64_t batch, int64_t n, int64_t s0, int64_t s1, int64_t s2)
   return (batch - 1) * s0 + (n - 1) * s1 + (n - 1) * s2 + 1;
 }
 
+// ---- opt-in per-launch profiling (fastqr_profile_*) ----------------------
+enum Kind { kCopy = 0, kPanel = 1, kUpdate = 2, kWave = 3, kLds = 4 };
+const char* const kKindNames[FASTQR_PROFILE_KINDS] = {"copy", "panel", "update", "wave64", "lds"};
+
+struct Record {
+  int kind;
+  hipEvent_t start, stop;
+  double flops, bytes;
+};
+
+struct Totals {
+  int64_t launches = 0;
+  double ms = 0.0, flops = 0.0, bytes = 0.0;
+};
+
+struct Profiler {
+  bool on = false;
+  std::vector<Record> pending;
+  std::vector<hipEvent_t> pool;
+  Totals totals[FASTQR_PROFILE_KINDS];
+
+  hipEvent_t take() {
+    if (!pool.empty()) {
+      hipEvent_t e = pool.back();
+      pool.pop_back();
+      return e;
+    }
+    hipEvent_t e = nullptr;
+    if (hipEventCreate(&e) != hipSuccess) return nullptr;
+    return e;
+  }
+
+  hipError_t drain() {
+    hipError_t err = hipSuccess;
+    for (Record& r : pending) {
+      float ms = 0.0f;
+      hipError_t e = hipEventSynchronize(r.stop);
+      if (e == hipSuccess) e = hipEventElapsedTime(&ms, r.start, r.stop);
+      if (e != hipSuccess && err == hipSuccess) err = e;
+      Totals& t = totals[r.kind];
+      t.launches += 1;
+      t.ms += ms;
+      t.flops += r.flops;
+      t.bytes += r.bytes;
+      pool.push_back(r.start);
+      pool.push_back(r.stop);
+    }
+    pending.clear();
+    return err;
+  }
+};
+
+thread_local Profiler g_prof;
+
+// Launch `fn` (returning hipError_t), bracketed by events when profiling.
+template <class F>
+hipError_t timed(int kind, double flops, double bytes, hipStream_t stream, F&& fn) {
+  if (!g_prof.on) return fn();
+  hipEvent_t a = g_prof.take(), b = g_prof.take();
+  if (!a || !b) return fn();
+  (void)hipEventRecord(a, stream);
+  const hipError_t e = fn();
+  (void)hipEventRecord(b, stream);
+  g_prof.pending.push_back(Record{kind, a, b, flops, bytes});
+  return e;
+}
+
 }  // namespace
 
 extern "C" {
+
+int fastqr_profile_enable(int on) {
+  if (on) {
+    (void)g_prof.drain();
+    for (Totals& t : g_prof.totals) t = Totals{};
+  }
+  g_prof.on = on != 0;
+  return FASTQR_OK;
+}
+
+int fastqr_profile_collect(int kind, int64_t* launches, double* milliseconds, double* flops, double* bytes) {
+  if (kind < 0 || kind >= FASTQR_PROFILE_KINDS) return fail(FASTQR_EINVAL, "profile kind %d out of range", kind);
+  const hipError_t e = g_prof.drain();
+  const Totals& t = g_prof.totals[kind];
+  if (launches) *launches = t.launches;
+  if (milliseconds) *milliseconds = t.ms;
+  if (flops) *flops = t.flops;
+  if (bytes) *bytes = t.bytes;
+  return e == hipSuccess ? FASTQR_OK : hip_fail(e, "profile collect");
+}
+
+const char* fastqr_profile_kind_name(int kind) {
+  return (kind >= 0 && kind < FASTQR_PROFILE_KINDS) ? kKindNames[kind] : "";
+}
 
 int fastqr_version(void) { return 1; }
 
@@ -95,8 +188,12 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
     const bool same = (A == H && a_s0 == h_s0 && a_s1 == h_s1 && a_s2 == h_s2);
     if (!same && ranges_overlap(A, span_elems(batch, n, a_s0, a_s1, a_s2), H, span_elems(batch, n, h_s0, h_s1, h_s2)))
       return fail(FASTQR_EOVERLAP, "A and H overlap with different layouts");
-    const hipError_t e = fastqr::launch_qr_wave(A, batch, ni, a_s0, a_s1, a_s2, H, h_s0, h_s1, h_s2, tau,
-                                                tau_s0, tau_s1, stream);
+    const double nn = (double)n;
+    const hipError_t e = timed(kWave, batch * 4.0 * nn * nn * nn / 3.0, batch * (8.0 * nn * nn + 4.0 * nn), stream,
+                               [&] {
+                                 return fastqr::launch_qr_wave(A, batch, ni, a_s0, a_s1, a_s2, H, h_s0, h_s1, h_s2,
+                                                               tau, tau_s0, tau_s1, stream);
+                               });
     return e == hipSuccess ? FASTQR_OK : hip_fail(e, "qr_wave launch");
   }
 
@@ -119,16 +216,28 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   float* Tws = (float*)workspace;
   const bool vec = ((uintptr_t)H % 16 == 0) && (h_s0 % 4 == 0) && (h_s2 % 4 == 0) && (n % 4 == 0);
   hipError_t e = hipSuccess;
+  const double bd = (double)batch;
   if (!same) {
-    e = fastqr::launch_copy_colmajor(A, batch, ni, a_s0, a_s1, a_s2, H, h_s0, h_s2, stream);
+    e = timed(kCopy, 0.0, bd * 8.0 * (double)n * (double)n, stream, [&] {
+      return fastqr::launch_copy_colmajor(A, batch, ni, a_s0, a_s1, a_s2, H, h_s0, h_s2, stream);
+    });
     if (e != hipSuccess) return hip_fail(e, "copy launch");
   }
   for (int k0 = 0; k0 < ni;) {
     const int nb = fastqr::panel_width_for(ni - k0);
-    e = fastqr::launch_panel(H, batch, h_s0, h_s2, tau, tau_s0, tau_s1, Tws, ni, k0, stream);
+    const double m = ni - k0;
+    const double wd = (m < nb) ? m : nb;
+    const double c = m - wd;
+    e = timed(kPanel, bd * (2.0 * m * wd * wd - 2.0 * wd * wd * wd / 3.0), bd * 8.0 * m * wd, stream, [&] {
+      return fastqr::launch_panel(H, batch, h_s0, h_s2, tau, tau_s0, tau_s1, Tws, ni, k0, stream);
+    });
     if (e != hipSuccess) return hip_fail(e, "panel launch");
-    e = fastqr::launch_update(H, batch, h_s0, h_s2, Tws, ni, k0, nb, vec, stream);
-    if (e != hipSuccess) return hip_fail(e, "update launch");
+    if (c > 0) {
+      e = timed(kUpdate, bd * 4.0 * m * wd * c, bd * (8.0 * m * c + 4.0 * m * wd), stream, [&] {
+        return fastqr::launch_update(H, batch, h_s0, h_s2, Tws, ni, k0, nb, vec, stream);
+      });
+      if (e != hipSuccess) return hip_fail(e, "update launch");
+    }
     k0 += nb;
   }
   return FASTQR_OK;

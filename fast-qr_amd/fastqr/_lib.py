@@ -31,7 +31,11 @@ EXPORTED_SYMBOLS = (
     "fastqr_last_error",
     "fastqr_version",
     "fastqr_debug_force_error",
+    "fastqr_profile_enable",
+    "fastqr_profile_collect",
+    "fastqr_profile_kind_name",
 )
+PROFILE_KINDS = ("copy", "panel", "update", "wave64", "lds")
 
 
 class FastQRUnavailable(RuntimeError):
@@ -76,6 +80,13 @@ def cdll() -> ctypes.CDLL:
         lib.fastqr_version.restype = ctypes.c_int
         lib.fastqr_debug_force_error.argtypes = [ctypes.c_int]
         lib.fastqr_debug_force_error.restype = None
+        lib.fastqr_profile_enable.argtypes = [ctypes.c_int]
+        lib.fastqr_profile_enable.restype = ctypes.c_int
+        dp = ctypes.POINTER(ctypes.c_double)
+        lib.fastqr_profile_collect.argtypes = [ctypes.c_int, ctypes.POINTER(ctypes.c_int64), dp, dp, dp]
+        lib.fastqr_profile_collect.restype = ctypes.c_int
+        lib.fastqr_profile_kind_name.argtypes = [ctypes.c_int]
+        lib.fastqr_profile_kind_name.restype = ctypes.c_char_p
         _cdll = lib
     return _cdll
 
@@ -98,6 +109,25 @@ def ext():
         sys.modules.setdefault("fastqr._fastqr_py", mod)
         _ext = mod
     return _ext
+
+
+def profile_enable(on: bool) -> None:
+    cdll().fastqr_profile_enable(1 if on else 0)
+
+
+def profile_collect() -> dict[str, dict[str, float]]:
+    """Per kernel kind: launches, ms (summed kernel time), flops, bytes."""
+    lib = cdll()
+    out = {}
+    for kind, name in enumerate(PROFILE_KINDS):
+        launches = ctypes.c_int64()
+        ms, fl, by = ctypes.c_double(), ctypes.c_double(), ctypes.c_double()
+        rc = lib.fastqr_profile_collect(kind, ctypes.byref(launches), ctypes.byref(ms), ctypes.byref(fl),
+                                        ctypes.byref(by))
+        if rc != 0:
+            raise FastQRError(rc, lib.fastqr_last_error().decode())
+        out[name] = {"launches": launches.value, "ms": ms.value, "flops": fl.value, "bytes": by.value}
+    return out
 
 
 def loaded_paths() -> list[str]:

@@ -52,10 +52,12 @@ def haar(n: int, gen: torch.Generator, count: int = 1) -> torch.Tensor:
 def svd_structured(n: int, singular: torch.Tensor, gen: torch.Generator, count: int) -> torch.Tensor:
     """`count` matrices U diag(s) V^T with Haar U, V, returned in fp32."""
     out = torch.empty((count, n, n), dtype=torch.float32)
-    for i in range(count):
-        u = haar(n, gen)[0]
-        v = haar(n, gen)[0]
-        out[i] = ((u * singular.unsqueeze(0)) @ v.T).to(torch.float32)
+    chunk = 32
+    for s0 in range(0, count, chunk):
+        k = min(chunk, count - s0)
+        u = haar(n, gen, k)
+        v = haar(n, gen, k)
+        out[s0 : s0 + k] = ((u * singular.reshape(1, 1, n)) @ v.transpose(-1, -2)).to(torch.float32)
     return out
 
 

@@ -101,6 +101,25 @@ int fastqr_version(void);
  */
 void fastqr_debug_force_error(int code);
 
+/*
+ * Profiling hooks (no counterpart in the reference; the reference times only
+ * whole calls with CUDA events, official/eval.py:200-206).  While enabled,
+ * every kernel launch that fastqr_geqrf_f32 makes on the calling thread is
+ * bracketed by hipEvents recorded on the launch stream, and its algorithmic
+ * work (flops, HBM bytes) is accumulated per kernel kind.  Recording events
+ * adds a little host work per launch; leave it disabled for headline timing.
+ *
+ * fastqr_profile_enable(on)   1 starts a fresh collection, 0 stops recording.
+ * fastqr_profile_collect(kind, ...)  waits for the recorded events and returns
+ *   launch count, summed kernel milliseconds, and summed algorithmic flops and
+ *   bytes for kind `kind` (0 .. FASTQR_PROFILE_KINDS-1); returns 0 or a status.
+ * fastqr_profile_kind_name(kind)  "copy", "panel", "update", "wave64", "lds".
+ */
+#define FASTQR_PROFILE_KINDS 5
+int fastqr_profile_enable(int on);
+int fastqr_profile_collect(int kind, int64_t* launches, double* milliseconds, double* flops, double* bytes);
+const char* fastqr_profile_kind_name(int kind);
+
 #ifdef __cplusplus
 }
 #endif
