@@ -1,8 +1,8 @@
 // device.hpp — shared gfx950 device helpers for the batched QR kernels.
 //
 // Wave64 only (CDNA4).  Cross-lane moves use DPP row/quad permutes and
-// ds_swizzle where a fixed xor pattern fits inside 32 lanes, ds_bpermute
-// (__shfl_xor) for the xor-32 step.
+// ds_swizzle where a fixed xor pattern fits inside 32 lanes, and gfx950's
+// v_permlane32_swap for the xor-32 step.
 #pragma once
 
 #include <hip/hip_runtime.h>
@@ -14,11 +14,15 @@ constexpr int kWave = 64;
 
 typedef float f32x4 __attribute__((ext_vector_type(4)));
 typedef float f32x16 __attribute__((ext_vector_type(16)));
+typedef float v32 __attribute__((ext_vector_type(32)));
 
 // Householder reflector in the reference's convention (LAPACK slarfg without
 // the safmin rescaling loop; submissions/candidate.py:654-668, 2084-2098).
 // `inv` scales x into v (v = x * inv); the reference divides by
 // (alpha - beta), LAPACK multiplies by its reciprocal — the latter is used.
+// The square root and both reciprocals are the hardware v_sqrt_f32 /
+// v_rcp_f32 (<= 1 ulp each; the arguments are far from the denormal range for
+// any input whose squared column norms are representable).
 struct Reflector {
   float beta;
   float tau;
@@ -28,10 +32,10 @@ struct Reflector {
 __device__ __forceinline__ Reflector make_reflector(float alpha, float sigma) {
   Reflector r;
   if (sigma > 0.0f) {
-    const float norm = sqrtf(alpha * alpha + sigma);
+    const float norm = __builtin_amdgcn_sqrtf(fmaf(alpha, alpha, sigma));
     r.beta = (alpha >= 0.0f) ? -norm : norm;
-    r.tau = (r.beta - alpha) / r.beta;
-    r.inv = 1.0f / (alpha - r.beta);
+    r.tau = (r.beta - alpha) * __builtin_amdgcn_rcpf(r.beta);
+    r.inv = __builtin_amdgcn_rcpf(alpha - r.beta);
   } else {
     r.beta = alpha;
     r.tau = 0.0f;
@@ -57,13 +61,24 @@ __device__ __forceinline__ float xor_lane(float v) {
     // ds_swizzle bit-mask mode inside 32-lane halves: and 0x1f, or 0, xor OFF
     return __int_as_float(__builtin_amdgcn_ds_swizzle(__float_as_int(v), 0x1F | (OFF << 10)));
   } else {
-    return __shfl_xor(v, OFF, kWave);
+    // xor 32 with v_permlane32_swap(v, v): the first result keeps lanes 0-31
+    // and receives lanes 0-31 into 32-63; the second receives lanes 32-63 into
+    // 0-31 and keeps 32-63.
+    const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+    return __uint_as_float((__lane_id() < 32) ? r[1] : r[0]);
   }
+}
+
+// v(lane) + v(lane ^ 32) in every lane: the two results of one
+// v_permlane32_swap are exactly {v_l, v_(l^32)} in some order per half.
+__device__ __forceinline__ float xor32_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
 // Sum over all 64 lanes, result in every lane.
 __device__ __forceinline__ float wave_sum(float v) {
-  v += xor_lane<32>(v);
+  v = xor32_sum(v);
   v += xor_lane<16>(v);
   v += xor_lane<8>(v);
   v += xor_lane<4>(v);
@@ -115,6 +130,38 @@ __device__ __forceinline__ float wave_transpose_reduce(float* p, int lane) {
 template <int NB>
 __device__ __forceinline__ constexpr int reduce_shift() {
   return NB == 1 ? 6 : NB == 2 ? 5 : NB == 4 ? 4 : NB == 8 ? 3 : NB == 16 ? 2 : NB == 32 ? 1 : 0;
+}
+
+// ---- buffer addressing: one SGPR descriptor per matrix, 32-bit byte offsets
+// per lane.  An offset at or beyond `bytes` reads 0 and drops stores
+// (hardware range check), so masked lanes use kOffNone instead of a branch.
+typedef __amdgpu_buffer_rsrc_t rsrc_t;
+constexpr uint32_t kOffNone = 0x80000000u;
+// descriptor word 3 for raw (untyped) access on GFX9-family parts
+constexpr int kRsrcWord3 = 0x00020000;
+
+__device__ __forceinline__ rsrc_t make_rsrc(const void* base, uint32_t bytes) {
+  return __builtin_amdgcn_make_buffer_rsrc(const_cast<void*>(base), (short)0, (int)bytes, kRsrcWord3);
+}
+__device__ __forceinline__ float buf_load(rsrc_t r, uint32_t off) {
+  return __uint_as_float(__builtin_amdgcn_raw_buffer_load_b32(r, (int)off, 0, 0));
+}
+__device__ __forceinline__ f32x4 buf_load4(rsrc_t r, uint32_t off) {
+  const auto v = __builtin_amdgcn_raw_buffer_load_b128(r, (int)off, 0, 0);
+  f32x4 out;
+  out[0] = __uint_as_float(v[0]);
+  out[1] = __uint_as_float(v[1]);
+  out[2] = __uint_as_float(v[2]);
+  out[3] = __uint_as_float(v[3]);
+  return out;
+}
+__device__ __forceinline__ void buf_store(rsrc_t r, uint32_t off, float v) {
+  __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(v), r, (int)off, 0, 0);
+}
+__device__ __forceinline__ void buf_store4(rsrc_t r, uint32_t off, f32x4 v) {
+  typedef unsigned int u32x4 __attribute__((ext_vector_type(4)));
+  u32x4 u = {__float_as_uint(v[0]), __float_as_uint(v[1]), __float_as_uint(v[2]), __float_as_uint(v[3])};
+  __builtin_amdgcn_raw_buffer_store_b128(u, r, (int)off, 0, 0);
 }
 
 __device__ __forceinline__ float readlane(float v, int lane) {

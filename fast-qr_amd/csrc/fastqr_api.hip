@@ -154,7 +154,7 @@ const char* fastqr_path_name(int64_t n) {
 
 size_t fastqr_workspace_bytes(int64_t batch, int64_t n) {
   if (batch <= 0 || n <= kWaveMaxN) return 0;
-  const size_t t_bytes = (size_t)batch * fastqr::kMaxPanel * fastqr::kMaxPanel * sizeof(float);
+  const size_t t_bytes = (size_t)batch * fastqr::kMaxSlots * 32 * 32 * sizeof(float);
   return (t_bytes + 255) & ~(size_t)255;
 }
 
@@ -202,6 +202,9 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
     return fail(FASTQR_ELAYOUT,
                 "H must have contiguous columns (stride (*, 1, >=n)); got (%lld, %lld, %lld)",
                 (long long)h_s0, (long long)h_s1, (long long)h_s2);
+  if (h_s2 * n * 4 >= (int64_t)1 << 31)
+    return fail(FASTQR_ELAYOUT, "one matrix of H spans %lld bytes; the blocked path addresses at most 2 GiB",
+                (long long)(h_s2 * n * 4));
   if (batch > 1 && h_s0 < h_s2 * n)
     return fail(FASTQR_ELAYOUT, "H batch stride %lld smaller than one matrix (%lld)", (long long)h_s0,
                 (long long)(h_s2 * n));
@@ -223,22 +226,41 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
     });
     if (e != hipSuccess) return hip_fail(e, "copy launch");
   }
-  for (int k0 = 0; k0 < ni;) {
-    const int nb = fastqr::panel_width_for(ni - k0);
-    const double m = ni - k0;
-    const double wd = (m < nb) ? m : nb;
-    const double c = m - wd;
-    e = timed(kPanel, bd * (2.0 * m * wd * wd - 2.0 * wd * wd * wd / 3.0), bd * 8.0 * m * wd, stream, [&] {
-      return fastqr::launch_panel(H, batch, h_s0, h_s2, tau, tau_s0, tau_s1, Tws, ni, k0, stream);
-    });
-    if (e != hipSuccess) return hip_fail(e, "panel launch");
-    if (c > 0) {
-      e = timed(kUpdate, bd * 4.0 * m * wd * c, bd * (8.0 * m * c + 4.0 * m * wd), stream, [&] {
-        return fastqr::launch_update(H, batch, h_s0, h_s2, Tws, ni, k0, nb, vec, stream);
+  // Panels are processed in groups of up to kMaxWY: each panel is followed by
+  // a narrow update of the rest of its group's columns; after the group, one
+  // wide update applies all of the group's transforms to the trailing columns.
+  for (int g0 = 0; g0 < ni;) {
+    const int mg = ni - g0;
+    const int nb = fastqr::panel_width_for(mg);
+    const int g_end = (g0 + fastqr::kMaxWY * nb < ni) ? g0 + fastqr::kMaxWY * nb : ni;
+    int npan = 0;
+    for (int pk = g0; pk < g_end; pk += nb, ++npan) {
+      const double m = ni - pk;
+      const double wd = (m < nb) ? m : nb;
+      e = timed(kPanel, bd * (2.0 * m * wd * wd - 2.0 * wd * wd * wd / 3.0), bd * 8.0 * m * wd, stream, [&] {
+        return fastqr::launch_panel(H, batch, h_s0, h_s2, tau, tau_s0, tau_s1, Tws, ni, pk, nb, mg, npan, vec,
+                                    stream);
+      });
+      if (e != hipSuccess) return hip_fail(e, "panel launch");
+      const int c0 = pk + (int)wd;
+      if (c0 < g_end) {
+        const double c = g_end - c0;
+        e = timed(kUpdate, bd * 4.0 * m * wd * c, bd * (8.0 * m * c + 4.0 * m * wd), stream, [&] {
+          return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, pk, nb, npan, 1, c0, g_end, vec, stream);
+        });
+        if (e != hipSuccess) return hip_fail(e, "update launch");
+      }
+    }
+    if (g_end < ni) {
+      const double m = mg;
+      const double wg = g_end - g0;
+      const double c = ni - g_end;
+      e = timed(kUpdate, bd * 4.0 * m * wg * c, bd * (8.0 * m * c + 4.0 * m * wg), stream, [&] {
+        return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, g0, nb, 0, npan, g_end, ni, vec, stream);
       });
       if (e != hipSuccess) return hip_fail(e, "update launch");
     }
-    k0 += nb;
+    g0 = g_end;
   }
   return FASTQR_OK;
 }

@@ -15,12 +15,20 @@ hipError_t launch_qr_wave(const float* A, int64_t batch, int n, int64_t as0, int
 hipError_t launch_copy_colmajor(const float* A, int64_t batch, int n, int64_t as0, int64_t as1, int64_t as2,
                                 float* H, int64_t hs0, int64_t ldh, hipStream_t stream);
 int panel_width_for(int m);
+// Panel of width nb at column k0, template sized for m_cap >= n - k0 rows;
+// its T factor goes to workspace slot `slot`.
 hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float* tau, int64_t ts0,
-                        int64_t ts1, float* Tws, int n, int k0, hipStream_t stream);
-hipError_t launch_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n, int k0,
-                         int nb, bool vec, hipStream_t stream);
+                        int64_t ts1, float* Tws, int n, int k0, int nb, int m_cap, int slot, bool vec,
+                        hipStream_t stream);
+// Apply nwy compact-WY transforms (panels k0 + i*nb, T slots slot0 + i) to
+// columns [c_begin, c_end), rows [k0, n).
+hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n,
+                            int k0, int nb, int slot0, int nwy, int c_begin, int c_end, bool vec,
+                            hipStream_t stream);
 
-// Largest panel width used by the blocked path (sizes the T workspace).
-constexpr int kMaxPanel = 32;
+// Panels per group: the wide trailing update applies this many transforms at once.
+constexpr int kMaxWY = 4;
+// T-factor slots per matrix in the workspace (32 x 32 floats each).
+constexpr int kMaxSlots = kMaxWY;
 
 }  // namespace fastqr

@@ -7,16 +7,16 @@
 //
 // Per panel [k0, k0 + w) of width w <= NB:
 //   panel_kernel   one workgroup per matrix.  The (n-k0) x w panel lives in
-//                  VGPRs, rows spread over the threads.  Each column step does
-//                  ONE block reduction of NB values per thread,
-//                      part[c] = sum_{r>j} x_r * a_r[c]          (all c)
-//                  which yields sigma (c == j), the Gram row g_c used for the
-//                  update of later columns (c > j), and h_c = v_c^T x used for
-//                  the T factor (c < j).  The reference needs a reduction for
+//                  VGPRs, each lane owning a run of rows of one column.  Each
+//                  column step does ONE reduction per column c,
+//                      tot_c = sum_{r>j} x_r * a_r[c]            (all c)
+//                  which yields sigma (c == j), the Gram row used for the
+//                  update of later columns (c > j), and v_c^T x used for the
+//                  T factor (c < j).  The reference needs a reduction for
 //                  sigma plus one per chunk of columns (submissions/candidate.py:2437-2498)
 //                  and recomputes T in every trailing CTA (2544-2584); here T
-//                  is built once, column by column (slarft recurrence), and
-//                  stored in the workspace.
+//                  is built once per panel (slarft recurrence) and stored in
+//                  the workspace.
 //   update_kernel  grid = (32-column strips, batch).  A2 <- A2 - V (T^T (V^T A2))
 //                  with v_mfma_f32_32x32x2f32.  A2 tiles are held in the MFMA
 //                  accumulator layout and reused directly as the B operand of
@@ -66,132 +66,189 @@ __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __re
 // ---------------------------------------------------------------------------
 // Panel factorisation
 // ---------------------------------------------------------------------------
-template <int NB>
-__device__ __forceinline__ float pick(const float (&row)[NB], int j) {
-  float r = 0.0f;
-#pragma unroll
-  for (int c = 0; c < NB; ++c) r = (c == j) ? row[c] : r;
-  return r;
+// Layout: lane (chunk q, column c) holds rows [q*R, q*R + R) of panel column c
+// in R VGPRs (an ext_vector so a uniform row index lowers to s_set_gpr_idx).
+// A wave holds CPW = 64/NB chunks; the workgroup NW*CPW chunks.  At step j:
+//   1. the lanes of column j publish their (masked) rows of column j to a
+//      per-chunk LDS slot, read back by the lanes of the same chunk (same wave:
+//      no workgroup barrier);
+//   2. lane (q, c) forms the partial  sum_{r>j, r in q} x_r a_r[c]  and the
+//      chunk's copy of row j; partials are summed over the chunks of the wave
+//      with xor shuffles, then over waves through LDS (one barrier);
+//   3. every lane derives the reflector (alpha = row j of column j, sigma =
+//      total of column j) and, for its column c,
+//        z_c = a_j[c] + tot_c / (alpha - beta)
+//      which is v^T a_c for c > j (update scale) and v_c^T v for c < j (the
+//      slarft inputs, kept in LDS for the T factor built after the loop);
+//   4. updates its rows  a_r[c] -= tau z_c v_r  (column j itself is scaled
+//      into v in the same FMA pair) and row j.
+__device__ __forceinline__ void wave_lds_sync() {
+  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+  __builtin_amdgcn_wave_barrier();
+  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
 }
 
-template <int NB>
-__device__ __forceinline__ void place(float (&row)[NB], int j, float v) {
-#pragma unroll
-  for (int c = 0; c < NB; ++c) row[c] = (c == j) ? v : row[c];
-}
+template <int NB, int NW, int R, bool VEC>
+__global__ void __launch_bounds__(NW * 64) panel_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh,
+                                                        float* __restrict__ tau, int64_t ts0, int64_t ts1,
+                                                        float* __restrict__ Tws, int n, int k0, int slot) {
+  static_assert(64 % NB == 0 && NB <= 32 && R % 32 == 0, "layout: row j < NB must sit in chunk 0");
+  constexpr int CPW = 64 / NB;
+  constexpr int NCH = NW * CPW;
+  constexpr int XS = R + 4;  // padded chunk stride in LDS (spreads chunks over banks)
+  constexpr int NSUB = R / 32;
 
-// Rows of the panel (local index r = t + q*NT, q < RPT) live in registers
-// a[q][0..NB).  Writes the factored panel back into H, tau[k0..k0+w) and
-// T (NB x NB, row-major, zero padded) into Tws[b].
-template <int NB, int NT, int RPT>
-__global__ void __launch_bounds__(NT) panel_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh,
-                                                   float* __restrict__ tau, int64_t ts0, int64_t ts1,
-                                                   float* __restrict__ Tws, int n, int k0) {
-  constexpr int NW = NT / kWave;
-  constexpr int SHIFT = reduce_shift<NB>();
   const int64_t b = blockIdx.x;
   const int m = n - k0;
   const int w = m < NB ? m : NB;
-  const int t = threadIdx.x;
-  const int lane = t & (kWave - 1);
-  const int wave = t / kWave;
-  float* Hp = H + b * hs0 + (int64_t)k0 * ldh + k0;  // panel element (r, c) at Hp[c*ldh + r]
+  const int lane = threadIdx.x & 63;
+  const int wave = threadIdx.x >> 6;
+  const int c = lane % NB;
+  const int qw = lane / NB;
+  const int q = wave * CPW + qw;
+  const int row0 = q * R;
+  float* colp = H + b * hs0 + (int64_t)(k0 + c) * ldh + k0;
 
-  __shared__ float red[2][NW][NB];
-  __shared__ float rowbuf[2][NB];
+  __shared__ __attribute__((aligned(16))) float xs[NCH * XS];
+  __shared__ float2 red[2][NW][NB];
+  __shared__ float ys[NB][NB + 1];
+  __shared__ float taus[NB];
 
-  float a[RPT][NB];
+  // rows held as NSUB sub-vectors of 32 so a uniform index stays in VGPRs
+  v32 av[NSUB];
+#define A_(i) av[(i) >> 5][(i) & 31]
+  const bool colok = c < w;
 #pragma unroll
-  for (int q = 0; q < RPT; ++q) {
-    const int r = t + q * NT;
+  for (int i = 0; i < R; i += 4) {
+    const int r = row0 + i;
+    if constexpr (VEC) {
+      f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
+      if (colok && r < m) v = *reinterpret_cast<const f32x4*>(colp + r);
+      A_(i) = v[0];
+      A_(i + 1) = v[1];
+      A_(i + 2) = v[2];
+      A_(i + 3) = v[3];
+    } else {
 #pragma unroll
-    for (int c = 0; c < NB; ++c) a[q][c] = (r < m && c < w) ? Hp[(int64_t)c * ldh + r] : 0.0f;
+      for (int u = 0; u < 4; ++u) A_(i + u) = (colok && r + u < m) ? colp[r + u] : 0.0f;
+    }
   }
-  float trow[NB];
-#pragma unroll
-  for (int c = 0; c < NB; ++c) trow[c] = 0.0f;
-  float tau_keep = 0.0f;
-  const int cidx = lane & (NB - 1);
+  float* xq = xs + q * XS;
 
   for (int j = 0; j < w; ++j) {
     const int par = j & 1;
-    float x[RPT];
+    // j < NB <= 32 <= R: row j is row j of chunk 0, element j of sub-vector 0
+    const int ju = __builtin_amdgcn_readfirstlane(j);
+    if (c == j) {
 #pragma unroll
-    for (int q = 0; q < RPT; ++q) {
-      const int r = t + q * NT;
-      const float xv = pick<NB>(a[q], j);
-      x[q] = (r > j) ? xv : 0.0f;
+      for (int i = 0; i < R; i += 4) {
+        f32x4 v;
+        v[0] = (row0 + i + 0 > j) ? A_(i + 0) : 0.0f;
+        v[1] = (row0 + i + 1 > j) ? A_(i + 1) : 0.0f;
+        v[2] = (row0 + i + 2 > j) ? A_(i + 2) : 0.0f;
+        v[3] = (row0 + i + 3 > j) ? A_(i + 3) : 0.0f;
+        *reinterpret_cast<f32x4*>(xq + i) = v;
+      }
     }
-    float part[NB];
+    wave_lds_sync();
+    float g0 = 0.0f, g1 = 0.0f, g2 = 0.0f, g3 = 0.0f;
 #pragma unroll
-    for (int c = 0; c < NB; ++c) {
-      float s = 0.0f;
-#pragma unroll
-      for (int q = 0; q < RPT; ++q) s = fmaf(x[q], a[q][c], s);
-      part[c] = s;
+    for (int i = 0; i < R; i += 4) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(xq + i);
+      g0 = fmaf(x[0], A_(i + 0), g0);
+      g1 = fmaf(x[1], A_(i + 1), g1);
+      g2 = fmaf(x[2], A_(i + 2), g2);
+      g3 = fmaf(x[3], A_(i + 3), g3);
     }
-    if (t == j) {
-#pragma unroll
-      for (int c = 0; c < NB; ++c) rowbuf[par][c] = a[0][c];
+    float g = (g0 + g1) + (g2 + g3);
+    float rowv = (q == 0) ? av[0][ju] : 0.0f;
+    if constexpr (CPW >= 2) {
+      if constexpr (NB == 32) {
+        g = xor32_sum(g);
+        rowv = xor32_sum(rowv);
+      } else {
+        g += xor_lane<NB>(g);
+        rowv += xor_lane<NB>(rowv);
+      }
     }
-    const float wsum = wave_transpose_reduce<NB>(part, lane);
-    if ((lane & ((1 << SHIFT) - 1)) == 0) red[par][wave][lane >> SHIFT] = wsum;
+    if constexpr (CPW >= 4) {
+      g += xor_lane<2 * NB>(g);
+      rowv += xor_lane<2 * NB>(rowv);
+    }
+    if constexpr (CPW >= 8) {
+      g += xor_lane<4 * NB>(g);
+      rowv += xor_lane<4 * NB>(rowv);
+    }
+    if (qw == 0) red[par][wave][c] = make_float2(g, rowv);
     __syncthreads();
-
-    float tot = 0.0f;
+    float tot = 0.0f, rowt = 0.0f;
 #pragma unroll
-    for (int wv = 0; wv < NW; ++wv) tot += red[par][wv][cidx];
-    const float row = rowbuf[par][cidx];
-    const float alpha = readlane(row, j);
-    const float sigma = readlane(tot, j);
-    const Reflector rf = make_reflector(alpha, sigma);
-    // lane c: c > j -> w_c = v^T a_c ; c < j -> y_c = v_c^T v
-    const float z = fmaf(tot, rf.inv, row);
-    const float s = (cidx > j && cidx < w) ? rf.tau * z : 0.0f;
-    float sc[NB];
-#pragma unroll
-    for (int c = 0; c < NB; ++c) sc[c] = readlane(s, c);
-
-#pragma unroll
-    for (int q = 0; q < RPT; ++q) {
-      const int r = t + q * NT;
-      const float v = (r > j) ? x[q] * rf.inv : (r == j ? 1.0f : 0.0f);
-      const float old = pick<NB>(a[q], j);
-#pragma unroll
-      for (int c = 0; c < NB; ++c) a[q][c] = fmaf(-sc[c], v, a[q][c]);
-      const float nv = (r > j) ? v : (r == j ? rf.beta : old);
-      place<NB>(a[q], j, nv);
+    for (int wv = 0; wv < NW; ++wv) {
+      const float2 t = red[par][wv][c];
+      tot += t.x;
+      rowt += t.y;
     }
+    const float sigma = readlane(tot, j);
+    const float alpha = readlane(rowt, j);
+    const Reflector rf = make_reflector(alpha, sigma);
+    const float z = fmaf(tot, rf.inv, rowt);
+    const float s = (c > j && c < w) ? rf.tau * z : 0.0f;
+    if (wave == 0 && qw == 0) {
+      ys[c][j] = z;
+      if (c == j) taus[j] = rf.tau;
+    }
+    // c == j: a <- (a - x) + x*inv  (exactly x*inv on rows > j, a elsewhere)
+    // c != j: a <- a + x * (-s*inv)
+    const bool isj = (c == j);
+    const float alp = isj ? rf.inv : -s * rf.inv;
+    const float bet = isj ? -1.0f : 0.0f;
+#pragma unroll
+    for (int i = 0; i < R; i += 4) {
+      const f32x4 x = *reinterpret_cast<const f32x4*>(xq + i);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) A_(i + u) = fmaf(x[u], alp, fmaf(bet, x[u], A_(i + u)));
+    }
+    if (q == 0) {
+      const float aj = av[0][ju];
+      av[0][ju] = isj ? rf.beta : aj - s;
+    }
+    // the next step's publish reuses xq: keep this step's reads ahead of it
+    wave_lds_sync();
+  }
 
-    if (wave == 0) {
+#pragma unroll
+  for (int i = 0; i < R; i += 4) {
+    const int r = row0 + i;
+    if constexpr (VEC) {
+      if (colok && r < m) {
+        f32x4 v = {A_(i), A_(i + 1), A_(i + 2), A_(i + 3)};
+        *reinterpret_cast<f32x4*>(colp + r) = v;
+      }
+    } else {
+#pragma unroll
+      for (int u = 0; u < 4; ++u)
+        if (colok && r + u < m) colp[r + u] = A_(i + u);
+    }
+  }
+
+#undef A_
+  // T factor (slarft recurrence) from the stored y_p^(j) = v_p^T v_j:
+  //   T[i][j] = -tau_j * sum_{i <= p < j} T[i][p] y_p^(j),  T[j][j] = tau_j
+  __syncthreads();
+  if (wave == 0 && lane < NB) {
+    float trow[NB];
+#pragma unroll
+    for (int jj = 0; jj < NB; ++jj) {
       float acc = 0.0f;
 #pragma unroll
-      for (int p = 0; p < NB; ++p) {
-        const float yp = readlane(z, p);
-        acc = fmaf(trow[p], (p < j) ? yp : 0.0f, acc);
-      }
-      const float tij = (lane < j) ? -rf.tau * acc : (lane == j ? rf.tau : 0.0f);
-      place<NB>(trow, j, tij);
-      if (lane == j) tau_keep = rf.tau;
+      for (int p = 0; p < jj; ++p) acc = fmaf(trow[p], ys[p][jj], acc);
+      const float tj = (jj < w) ? taus[jj] : 0.0f;
+      trow[jj] = (lane < jj) ? -tj * acc : (lane == jj ? tj : 0.0f);
     }
-  }
-
+    float* Tb = Tws + ((b * kMaxSlots + slot) * 32 + lane) * 32;
 #pragma unroll
-  for (int q = 0; q < RPT; ++q) {
-    const int r = t + q * NT;
-    if (r < m) {
-#pragma unroll
-      for (int c = 0; c < NB; ++c)
-        if (c < w) Hp[(int64_t)c * ldh + r] = a[q][c];
-    }
-  }
-  if (wave == 0) {
-    if (lane < w) tau[b * ts0 + (int64_t)(k0 + lane) * ts1] = tau_keep;
-    if (lane < NB) {
-      float* Tb = Tws + b * (NB * NB) + lane * NB;
-#pragma unroll
-      for (int c = 0; c < NB; ++c) Tb[c] = trow[c];
-    }
+    for (int jj = 0; jj < NB; ++jj) Tb[jj] = trow[jj];
+    if (lane < w) tau[b * ts0 + (int64_t)(k0 + lane) * ts1] = taus[lane];
   }
 }
 
@@ -255,11 +312,123 @@ __device__ __forceinline__ void store_ctile(float* __restrict__ Hb, int64_t ldh,
   }
 }
 
-template <int MT, bool VEC>
-__global__ void __launch_bounds__(256) update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh,
-                                                     const float* __restrict__ Tws, int tld, int n, int k0,
-                                                     int w) {
-  constexpr int MB = 32 * MT;  // padded reflector count
+// Applies `nwy` consecutive compact-WY transforms, panel i starting at row and
+// column kw = k0 + i*nb with width nb (<= 32) and T factor Tws slot
+// (slot0 + i), to the 32-column strip  [c_begin + 32*blockIdx.x, +32) of
+// columns in [c_begin, c_end), rows [k0, n).  The strip is split into 32-row
+// tiles; wave w owns tiles w, w+NW, ...  With RES the tiles stay in the MFMA
+// accumulator layout in VGPRs for all transforms (one load, one store per
+// element); otherwise (taller strips) every transform streams them twice.
+// Per transform:  P = V^T X  (16 MFMAs per tile, the X registers used as the
+// B operand through the contraction-index permutation), P summed over waves
+// in LDS, W = -(T^T P) (16 MFMAs), X += V W (16 MFMAs per tile).
+// Column-major matrix accessed through a buffer descriptor: element (row, col)
+// at byte offset 4 * (col * ldh + row).  n <= 8192 and ldh * n < 2^29 keep the
+// offsets within 32 bits (checked by the host).
+struct MatBuf {
+  rsrc_t r;
+  int ldh;
+  int n;
+  __device__ __forceinline__ uint32_t off(int row, int col) const { return 4u * (uint32_t)(col * ldh + row); }
+};
+
+// 32-row tile of column `col` (rows r0.., MFMA accumulator layout: register
+// 4q+i <- row r0 + 8q + 4h + i); rows >= n and !ok read as 0.
+template <bool VEC>
+__device__ __forceinline__ f32x16 tile_load(const MatBuf& M, int r0, int col, bool ok, int h) {
+  f32x16 x;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int rb = r0 + 8 * q + 4 * h;
+    if constexpr (VEC) {
+      const f32x4 v = buf_load4(M.r, (ok && rb < M.n) ? M.off(rb, col) : kOffNone);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[4 * q + i] = v[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[4 * q + i] = buf_load(M.r, (ok && rb + i < M.n) ? M.off(rb + i, col) : kOffNone);
+    }
+  }
+  return x;
+}
+
+template <bool VEC>
+__device__ __forceinline__ void tile_store(const MatBuf& M, int r0, int col, bool ok, int h, const f32x16& x) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int rb = r0 + 8 * q + 4 * h;
+    if constexpr (VEC) {
+      f32x4 v = {x[4 * q + 0], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]};
+      buf_store4(M.r, (ok && rb < M.n) ? M.off(rb, col) : kOffNone, v);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) buf_store(M.r, (ok && rb + i < M.n) ? M.off(rb + i, col) : kOffNone, x[4 * q + i]);
+    }
+  }
+}
+
+// P += V^T X for one 32-row tile at r0 of the transform whose reflectors start
+// at row/column kw (width nb).  V pattern A: lane holds rows r0 + 8q + 4h + i
+// of reflector l32, loaded 4 rows at a time.
+template <bool VEC>
+__device__ __forceinline__ void wy_accumulate(f32x16& P, const f32x16& X, const MatBuf& M, int kw, int nb, int r0,
+                                              int h, int l32) {
+  const int refl = l32;
+  const bool active = refl < nb;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int rb = r0 + 8 * q + 4 * h;
+    f32x4 v;
+    if constexpr (VEC) {
+      v = buf_load4(M.r, (active && rb < M.n) ? M.off(rb, kw + refl) : kOffNone);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = buf_load(M.r, (active && rb + i < M.n) ? M.off(rb + i, kw + refl) : kOffNone);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rr = rb + i - kw;  // row within the transform's panel
+      const float vv = (rr < refl) ? 0.0f : (rr == refl ? 1.0f : v[i]);
+      P = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, X[4 * q + i], P, 0, 0, 0);
+    }
+  }
+}
+
+// X += V W for one tile.  V pattern B: lane holds row r0 + l32 of reflector
+// 8q + 4h + i.
+__device__ __forceinline__ void wy_apply(f32x16& X, const f32x16& W, const MatBuf& M, int kw, int nb, int r0, int h,
+                                         int l32) {
+  const int row = r0 + l32;
+  const int rr = row - kw;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float vb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int refl = 8 * q + 4 * h + i;
+      const bool load = refl < nb && rr > refl && row < M.n;
+      const float v = buf_load(M.r, load ? M.off(row, kw + refl) : kOffNone);
+      vb[i] = (refl < nb && rr == refl) ? 1.0f : v;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) X = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[i], W[4 * q + i], X, 0, 0, 0);
+  }
+}
+
+// Applies `nwy` consecutive compact-WY transforms, transform i starting at
+// row and column kw = k0 + i*nb with width nb (<= 32) and T factor in
+// workspace slot (slot0 + i), to the 32-column strip
+// [c_begin + 32*blockIdx.x, +32) of [c_begin, c_end), rows [k0, n).  The strip
+// is split into 32-row tiles; wave w owns tiles w, w+NW, ...  With RES the
+// tiles stay in VGPRs (MFMA accumulator layout) across all transforms: one
+// load and one store per element.  Without RES (taller strips) each transform
+// streams them twice.  Per transform: P = V^T X (the X registers are the B
+// operand, the contraction index permuted to match the accumulator layout),
+// P summed over waves in LDS, W = -(T^T P), X += V W.
+template <int NW, int TPW, bool RES, bool VEC>
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4, 8)))
+wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* __restrict__ Tws, int n, int k0,
+                 int nb, int slot0, int nwy, int c_begin, int c_end) {
   const int64_t b = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -267,95 +436,110 @@ __global__ void __launch_bounds__(256) update_kernel(float* __restrict__ H, int6
   const int l32 = lane & 31;
   const int m = n - k0;
   const int ntiles = (m + 31) >> 5;
-  const int col = k0 + w + 32 * blockIdx.x + l32;
-  const bool colok = col < n;
-  float* Hb = H + b * hs0;
+  const int col = c_begin + 32 * blockIdx.x + l32;
+  const bool colok = col < c_end;
+  const MatBuf M{make_rsrc(H + b * hs0, (uint32_t)(4 * ldh * n)), (int)ldh, n};
 
-  __shared__ float Ts[MB][MB + 1];
-  __shared__ float Pp[4][MT][16][64];
+  __shared__ float Ts[kMaxWY][32][33];
+  __shared__ float Pp[NW > 1 ? NW : 1][16][64];
+  __shared__ float Pt[16][64];
 
-  const float* Tb = Tws + b * (int64_t)(tld * tld);
-  for (int idx = threadIdx.x; idx < MB * MB; idx += 256) {
-    const int i = idx / MB, jx = idx % MB;
-    Ts[i][jx] = (i < w && jx < w) ? Tb[i * tld + jx] : 0.0f;
+  for (int idx = threadIdx.x; idx < nwy * 32 * 32; idx += NW * 64) {
+    const int i = idx >> 10, r = (idx >> 5) & 31, cc = idx & 31;
+    Ts[i][r][cc] = (r < nb && cc < nb) ? Tws[((b * kMaxSlots + slot0 + i) * 32 + r) * 32 + cc] : 0.0f;
   }
 
-  // pass 1: P = V^T A2 (partial per wave over its row tiles)
-  f32x16 P[MT];
+  f32x16 X[TPW];
+  if constexpr (RES) {
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int i = 0; i < 16; ++i) P[mt][i] = 0.0f;
+    for (int t = 0; t < TPW; ++t) {
+      const int rt = wave + NW * t;
+      X[t] = tile_load<VEC>(M, k0 + 32 * rt, col, colok && rt < ntiles, h);
+    }
+  }
+  __syncthreads();
 
-  for (int rt = wave; rt < ntiles; rt += 4) {
-    const int r0 = k0 + 32 * rt;
-    float X[16];
-    load_ctile<VEC>(Hb, ldh, n, r0, col, colok, h, X);
+  for (int i = 0; i < nwy; ++i) {
+    const int kw = k0 + i * nb;
+    const int rt_first = (kw - k0) >> 5;  // tiles above this transform are untouched
+    // Row base made opaque per transform: the per-tile row indices and offsets
+    // are then recomputed (one add each) instead of being hoisted out of this
+    // loop and spilled.
+    int kb = k0;
+    asm volatile("" : "+v"(kb));
+    f32x16 P;
 #pragma unroll
-    for (int mt = 0; mt < MT; ++mt) {
-      const int refl = 32 * mt + l32;
-      float V[16];
-      if (refl < w) {
-        load_ctile<VEC>(Hb, ldh, n, r0, k0 + refl, true, h, V);
-      } else {
+    for (int j = 0; j < 16; ++j) P[j] = 0.0f;
+    if constexpr (RES) {
 #pragma unroll
-        for (int i = 0; i < 16; ++i) V[i] = 0.0f;
+      for (int t = 0; t < TPW; ++t) {
+        const int rt = wave + NW * t;
+        if (rt < ntiles && rt >= rt_first) wy_accumulate<VEC>(P, X[t], M, kw, nb, kb + 32 * rt, h, l32);
+        __builtin_amdgcn_sched_barrier(0);  // keep each tile's V loads next to its MFMAs
       }
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int rr = r0 + 8 * (j >> 2) + 4 * h + (j & 3) - k0;
-        const float vv = v_fix(V[j], rr, refl, w);
-        P[mt] = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, X[j], P[mt], 0, 0, 0);
+    } else {
+      for (int rt = wave; rt < ntiles; rt += NW) {
+        if (rt < rt_first) continue;
+        const f32x16 Xs = tile_load<VEC>(M, k0 + 32 * rt, col, colok, h);
+        wy_accumulate<VEC>(P, Xs, M, kw, nb, k0 + 32 * rt, h, l32);
       }
+    }
+    if constexpr (NW > 1) {
+      // sum over waves: each wave reduces 16/NW of the registers
+#pragma unroll
+      for (int j = 0; j < 16; ++j) Pp[wave][j][lane] = P[j];
+      __syncthreads();
+      constexpr int SL = 16 / NW;
+#pragma unroll
+      for (int jj = 0; jj < SL; ++jj) {
+        const int j = wave * SL + jj;
+        float acc = 0.0f;
+#pragma unroll
+        for (int wv = 0; wv < NW; ++wv) acc += Pp[wv][j][lane];
+        Pt[j][lane] = acc;
+      }
+      __syncthreads();
+#pragma unroll
+      for (int j = 0; j < 16; ++j) P[j] = Pt[j][lane];
+    }
+    f32x16 W;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) W[j] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int kk = 8 * (j >> 2) + 4 * h + (j & 3);
+      W = __builtin_amdgcn_mfma_f32_32x32x2f32(Ts[i][kk][l32], P[j], W, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) W[j] = -W[j];
+    if constexpr (RES) {
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const int rt = wave + NW * t;
+        if (rt < ntiles && rt >= rt_first) wy_apply(X[t], W, M, kw, nb, kb + 32 * rt, h, l32);
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else {
+      for (int rt = wave; rt < ntiles; rt += NW) {
+        if (rt < rt_first) continue;
+        f32x16 C = tile_load<VEC>(M, k0 + 32 * rt, col, colok, h);
+        wy_apply(C, W, M, kw, nb, k0 + 32 * rt, h, l32);
+        tile_store<VEC>(M, k0 + 32 * rt, col, colok, h, C);
+      }
+      // the next transform reloads what this wave stored
+      __syncthreads();
     }
   }
 
+  if constexpr (RES) {
+    // recompute the store offsets rather than keeping the load offsets alive
+    int kb = k0, cs = col;
+    asm volatile("" : "+v"(kb), "+v"(cs));
 #pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int j = 0; j < 16; ++j) Pp[wave][mt][j][lane] = P[mt][j];
-  __syncthreads();
-#pragma unroll
-  for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-    for (int j = 0; j < 16; ++j)
-      P[mt][j] = Pp[0][mt][j][lane] + Pp[1][mt][j][lane] + Pp[2][mt][j][lane] + Pp[3][mt][j][lane];
-
-  // W = -(T^T P)
-  f32x16 W[MT];
-#pragma unroll
-  for (int mo = 0; mo < MT; ++mo) {
-#pragma unroll
-    for (int i = 0; i < 16; ++i) W[mo][i] = 0.0f;
-#pragma unroll
-    for (int mi = 0; mi < MT; ++mi)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int kk = 32 * mi + 8 * (j >> 2) + 4 * h + (j & 3);
-        W[mo] = __builtin_amdgcn_mfma_f32_32x32x2f32(Ts[kk][32 * mo + l32], P[mi][j], W[mo], 0, 0, 0);
-      }
-#pragma unroll
-    for (int i = 0; i < 16; ++i) W[mo][i] = -W[mo][i];
-  }
-
-  // pass 2: A2 += V W   (W already negated)
-  for (int rt = wave; rt < ntiles; rt += 4) {
-    const int r0 = k0 + 32 * rt;
-    float X[16];
-    load_ctile<VEC>(Hb, ldh, n, r0, col, colok, h, X);
-    f32x16 C;
-#pragma unroll
-    for (int i = 0; i < 16; ++i) C[i] = X[i];
-    const int row = r0 + l32;
-#pragma unroll
-    for (int mt = 0; mt < MT; ++mt)
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int refl = 32 * mt + 8 * (j >> 2) + 4 * h + (j & 3);
-        const float vb = v_elem(Hb, ldh, n, k0, w, row, refl);
-        C = __builtin_amdgcn_mfma_f32_32x32x2f32(vb, W[mt][j], C, 0, 0, 0);
-      }
-    store_ctile<VEC>(Hb, ldh, n, r0, col, colok, h, C);
+    for (int t = 0; t < TPW; ++t) {
+      const int rt = wave + NW * t;
+      tile_store<VEC>(M, kb + 32 * rt, cs, colok && rt < ntiles, h, X[t]);
+    }
   }
 }
 
@@ -373,40 +557,88 @@ hipError_t launch_copy_colmajor(const float* A, int64_t batch, int n, int64_t as
 int panel_width_for(int m) { return m > 4096 ? 8 : (m > 2048 ? 16 : 32); }
 
 hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float* tau, int64_t ts0,
-                        int64_t ts1, float* Tws, int n, int k0, hipStream_t stream) {
-  const int m = n - k0;
+                        int64_t ts1, float* Tws, int n, int k0, int nb, int m_cap, int slot, bool vec,
+                        hipStream_t stream) {
+  // template chosen for m_cap rows (the tallest panel of its group) and width nb;
+  // rows covered = NW * (64 / NB) * R
+  const int m = m_cap;
   const dim3 grid((unsigned)batch);
-#define FASTQR_PANEL(NB, NT, RPT)                                                                       \
-  hipLaunchKernelGGL((panel_kernel<NB, NT, RPT>), grid, dim3(NT), 0, stream, H, hs0, ldh, tau, ts0, ts1, \
-                     Tws, n, k0)
-  if (m <= 256) {
-    FASTQR_PANEL(32, 256, 1);
-  } else if (m <= 512) {
-    FASTQR_PANEL(32, 256, 2);
-  } else if (m <= 1024) {
-    FASTQR_PANEL(32, 256, 4);
-  } else if (m <= 2048) {
-    FASTQR_PANEL(32, 512, 4);
-  } else if (m <= 4096) {
-    FASTQR_PANEL(16, 512, 8);
+#define FASTQR_PANEL(NB, NW, R)                                                                           \
+  do {                                                                                                    \
+    if (vec)                                                                                              \
+      hipLaunchKernelGGL((panel_kernel<NB, NW, R, true>), grid, dim3(NW * 64), 0, stream, H, hs0, ldh, tau, \
+                         ts0, ts1, Tws, n, k0, slot);                                                     \
+    else                                                                                                  \
+      hipLaunchKernelGGL((panel_kernel<NB, NW, R, false>), grid, dim3(NW * 64), 0, stream, H, hs0, ldh,    \
+                         tau, ts0, ts1, Tws, n, k0, slot);                                                \
+  } while (0)
+  if (nb == 32) {
+    if (m <= 128) {
+      FASTQR_PANEL(32, 2, 32);
+    } else if (m <= 256) {
+      FASTQR_PANEL(32, 4, 32);
+    } else if (m <= 512) {
+      FASTQR_PANEL(32, 4, 64);
+    } else if (m <= 1024) {
+      FASTQR_PANEL(32, 8, 64);
+    } else if (m <= 2048) {
+      FASTQR_PANEL(32, 16, 64);
+    } else {
+      return hipErrorInvalidValue;
+    }
+  } else if (nb == 16) {
+    if (m <= 2048) {
+      FASTQR_PANEL(16, 16, 32);
+    } else if (m <= 4096) {
+      FASTQR_PANEL(16, 16, 64);
+    } else {
+      return hipErrorInvalidValue;
+    }
+  } else if (nb == 8) {
+    if (m <= 4096) {
+      FASTQR_PANEL(8, 16, 32);
+    } else if (m <= 8192) {
+      FASTQR_PANEL(8, 16, 64);
+    } else {
+      return hipErrorInvalidValue;
+    }
   } else {
-    FASTQR_PANEL(8, 1024, 8);
+    return hipErrorInvalidValue;
   }
 #undef FASTQR_PANEL
   return hipGetLastError();
 }
 
-hipError_t launch_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n, int k0,
-                         int nb, bool vec, hipStream_t stream) {
-  const int w = (n - k0) < nb ? (n - k0) : nb;
-  const int trailing = n - k0 - w;
-  if (trailing <= 0) return hipSuccess;
-  const dim3 grid((unsigned)((trailing + 31) / 32), (unsigned)batch);
-  if (vec) {
-    hipLaunchKernelGGL((update_kernel<1, true>), grid, dim3(256), 0, stream, H, hs0, ldh, Tws, nb, n, k0, w);
+hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n,
+                            int k0, int nb, int slot0, int nwy, int c_begin, int c_end, bool vec,
+                            hipStream_t stream) {
+  const int cols = c_end - c_begin;
+  if (cols <= 0 || nwy <= 0) return hipSuccess;
+  const int ntiles = (n - k0 + 31) / 32;
+  const dim3 grid((unsigned)((cols + 31) / 32), (unsigned)batch);
+#define FASTQR_WY(NW, TPW, RES)                                                                             \
+  do {                                                                                                      \
+    if (vec)                                                                                                \
+      hipLaunchKernelGGL((wy_update_kernel<NW, TPW, RES, true>), grid, dim3(NW * 64), 0, stream, H, hs0, ldh, \
+                         Tws, n, k0, nb, slot0, nwy, c_begin, c_end);                                       \
+    else                                                                                                    \
+      hipLaunchKernelGGL((wy_update_kernel<NW, TPW, RES, false>), grid, dim3(NW * 64), 0, stream, H, hs0,    \
+                         ldh, Tws, n, k0, nb, slot0, nwy, c_begin, c_end);                                  \
+  } while (0)
+  if (ntiles <= 4) {
+    FASTQR_WY(1, 4, true);
+  } else if (ntiles <= 8) {
+    FASTQR_WY(2, 4, true);
+  } else if (ntiles <= 16) {
+    FASTQR_WY(4, 4, true);
+  } else if (ntiles <= 32) {
+    FASTQR_WY(8, 4, true);
+  } else if (ntiles <= 64) {
+    FASTQR_WY(16, 4, true);
   } else {
-    hipLaunchKernelGGL((update_kernel<1, false>), grid, dim3(256), 0, stream, H, hs0, ldh, Tws, nb, n, k0, w);
+    FASTQR_WY(16, 1, false);
   }
+#undef FASTQR_WY
   return hipGetLastError();
 }
 
