@@ -100,6 +100,36 @@ struct Profiler {
 
 thread_local Profiler g_prof;
 
+// ---- side stream and events for panel look-ahead (one set per device) ------
+struct DeviceAux {
+  hipStream_t side = nullptr;
+  std::vector<hipEvent_t> events;
+  size_t next = 0;
+  hipEvent_t take() {
+    if (next == events.size()) {
+      hipEvent_t e = nullptr;
+      if (hipEventCreateWithFlags(&e, hipEventDisableTiming) != hipSuccess) return nullptr;
+      events.push_back(e);
+    }
+    return events[next++];
+  }
+};
+
+thread_local std::vector<DeviceAux> g_aux;
+
+DeviceAux* device_aux() {
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess || dev < 0) return nullptr;
+  if ((size_t)dev >= g_aux.size()) g_aux.resize(dev + 1);
+  DeviceAux& a = g_aux[dev];
+  if (!a.side && hipStreamCreateWithFlags(&a.side, hipStreamNonBlocking) != hipSuccess) {
+    a.side = nullptr;
+    return nullptr;
+  }
+  a.next = 0;
+  return &a;
+}
+
 // Launch `fn` (returning hipError_t), bracketed by events when profiling.
 template <class F>
 hipError_t timed(int kind, double flops, double bytes, hipStream_t stream, F&& fn) {
@@ -226,41 +256,83 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
     });
     if (e != hipSuccess) return hip_fail(e, "copy launch");
   }
-  // Panels are processed in groups of up to kMaxWY: each panel is followed by
-  // a narrow update of the rest of its group's columns; after the group, one
-  // wide update applies all of the group's transforms to the trailing columns.
-  for (int g0 = 0; g0 < ni;) {
-    const int mg = ni - g0;
-    const int nb = fastqr::panel_width_for(mg);
+  // Panels are processed in groups of up to kMaxWY.  Within a group each
+  // panel is followed by a narrow update of the group's remaining columns;
+  // the group's transforms are then applied together to the columns right of
+  // it.  Look-ahead: that wide update is split into the next group's columns
+  // (first) and the rest; the next group's panels run on a side stream while
+  // the rest is updated on the caller's stream.  T slots alternate between
+  // two banks by group parity.
+  struct Group {
+    int g0, nb, g_end, npan, slot_base;
+  };
+  std::vector<Group> groups;
+  for (int g0 = 0, gi = 0; g0 < ni; ++gi) {
+    const int nb = fastqr::panel_width_for(ni - g0);
     const int g_end = (g0 + fastqr::kMaxWY * nb < ni) ? g0 + fastqr::kMaxWY * nb : ni;
-    int npan = 0;
-    for (int pk = g0; pk < g_end; pk += nb, ++npan) {
+    groups.push_back(Group{g0, nb, g_end, (g_end - g0 + nb - 1) / nb, (gi & 1) * fastqr::kMaxWY});
+    g0 = g_end;
+  }
+  auto run_panels = [&](const Group& G, hipStream_t st) -> hipError_t {
+    for (int i = 0; i < G.npan; ++i) {
+      const int pk = G.g0 + i * G.nb;
       const double m = ni - pk;
-      const double wd = (m < nb) ? m : nb;
-      e = timed(kPanel, bd * (2.0 * m * wd * wd - 2.0 * wd * wd * wd / 3.0), bd * 8.0 * m * wd, stream, [&] {
-        return fastqr::launch_panel(H, batch, h_s0, h_s2, tau, tau_s0, tau_s1, Tws, ni, pk, nb, mg, npan, vec,
-                                    stream);
+      const double wd = (m < G.nb) ? m : G.nb;
+      hipError_t err = timed(kPanel, bd * (2.0 * m * wd * wd - 2.0 * wd * wd * wd / 3.0), bd * 8.0 * m * wd, st, [&] {
+        return fastqr::launch_panel(H, batch, h_s0, h_s2, tau, tau_s0, tau_s1, Tws, ni, pk, G.nb, ni - pk,
+                                    G.slot_base + i, vec, st);
       });
-      if (e != hipSuccess) return hip_fail(e, "panel launch");
+      if (err != hipSuccess) return err;
       const int c0 = pk + (int)wd;
-      if (c0 < g_end) {
-        const double c = g_end - c0;
-        e = timed(kUpdate, bd * 4.0 * m * wd * c, bd * (8.0 * m * c + 4.0 * m * wd), stream, [&] {
-          return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, pk, nb, npan, 1, c0, g_end, vec, stream);
+      if (c0 < G.g_end) {
+        const double c = G.g_end - c0;
+        err = timed(kUpdate, bd * 4.0 * m * wd * c, bd * (8.0 * m * c + 4.0 * m * wd), st, [&] {
+          return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, pk, G.nb, G.slot_base + i, 1, c0, G.g_end,
+                                          vec, st);
         });
-        if (e != hipSuccess) return hip_fail(e, "update launch");
+        if (err != hipSuccess) return err;
       }
     }
-    if (g_end < ni) {
-      const double m = mg;
-      const double wg = g_end - g0;
-      const double c = ni - g_end;
-      e = timed(kUpdate, bd * 4.0 * m * wg * c, bd * (8.0 * m * c + 4.0 * m * wg), stream, [&] {
-        return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, g0, nb, 0, npan, g_end, ni, vec, stream);
-      });
-      if (e != hipSuccess) return hip_fail(e, "update launch");
+    return hipSuccess;
+  };
+  auto run_update = [&](const Group& G, int c_begin, int c_end, hipStream_t st) -> hipError_t {
+    if (c_end <= c_begin) return hipSuccess;
+    const double m = ni - G.g0, wg = G.g_end - G.g0, c = c_end - c_begin;
+    return timed(kUpdate, bd * 4.0 * m * wg * c, bd * (8.0 * m * c + 4.0 * m * wg), st, [&] {
+      return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, G.g0, G.nb, G.slot_base, G.npan, c_begin,
+                                      c_end, vec, st);
+    });
+  };
+
+  DeviceAux* aux = groups.size() > 2 ? device_aux() : nullptr;
+  if (!aux) {
+    for (const Group& G : groups) {
+      e = run_panels(G, stream);
+      if (e == hipSuccess) e = run_update(G, G.g_end, ni, stream);
+      if (e != hipSuccess) return hip_fail(e, "blocked launch");
     }
-    g0 = g_end;
+    return FASTQR_OK;
+  }
+  const hipStream_t side = aux->side;
+  hipEvent_t ev = aux->take();
+  if (!ev) return fail(FASTQR_EINVAL, "cannot create HIP events");
+  // the side stream must not run ahead of work already queued on `stream`
+  if ((e = hipEventRecord(ev, stream)) != hipSuccess || (e = hipStreamWaitEvent(side, ev, 0)) != hipSuccess)
+    return hip_fail(e, "stream join");
+  e = run_panels(groups[0], stream);
+  if (e != hipSuccess) return hip_fail(e, "panel launch");
+  for (size_t g = 0; g + 1 < groups.size(); ++g) {
+    const Group& G = groups[g];
+    const Group& Nx = groups[g + 1];
+    hipEvent_t ev_next = aux->take(), ev_pan = aux->take();
+    if (!ev_next || !ev_pan) return fail(FASTQR_EINVAL, "cannot create HIP events");
+    if ((e = run_update(G, Nx.g0, Nx.g_end, stream)) != hipSuccess) return hip_fail(e, "update launch");
+    if ((e = hipEventRecord(ev_next, stream)) != hipSuccess || (e = hipStreamWaitEvent(side, ev_next, 0)) != hipSuccess)
+      return hip_fail(e, "stream join");
+    if ((e = run_panels(Nx, side)) != hipSuccess) return hip_fail(e, "panel launch");
+    if ((e = hipEventRecord(ev_pan, side)) != hipSuccess) return hip_fail(e, "stream join");
+    if ((e = run_update(G, Nx.g_end, ni, stream)) != hipSuccess) return hip_fail(e, "update launch");
+    if ((e = hipStreamWaitEvent(stream, ev_pan, 0)) != hipSuccess) return hip_fail(e, "stream join");
   }
   return FASTQR_OK;
 }

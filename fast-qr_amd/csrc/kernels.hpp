@@ -28,7 +28,9 @@ hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, c
 
 // Panels per group: the wide trailing update applies this many transforms at once.
 constexpr int kMaxWY = 4;
-// T-factor slots per matrix in the workspace (32 x 32 floats each).
-constexpr int kMaxSlots = kMaxWY;
+// T-factor slots per matrix in the workspace (32 x 32 floats each): two
+// groups' worth, so one group's panels can run while the previous group's
+// transforms are still being applied.
+constexpr int kMaxSlots = 2 * kMaxWY;
 
 }  // namespace fastqr

@@ -78,10 +78,12 @@ __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __re
 //   3. every lane derives the reflector (alpha = row j of column j, sigma =
 //      total of column j) and, for its column c,
 //        z_c = a_j[c] + tot_c / (alpha - beta)
-//      which is v^T a_c for c > j (update scale) and v_c^T v for c < j (the
-//      slarft inputs, kept in LDS for the T factor built after the loop);
-//   4. updates its rows  a_r[c] -= tau z_c v_r  (column j itself is scaled
-//      into v in the same FMA pair) and row j.
+//      which is v^T a_c for c > j (update scale) and, times 1/(alpha_c -
+//      beta_c), v_c^T v for c < j (the slarft inputs, kept in LDS for the T
+//      factor built after the loop);
+//   4. updates its rows  a_r[c] -= tau z_c v_r  and row j.
+// A finished column keeps its unscaled x below the diagonal (no per-step
+// scaling pass); it is multiplied by its 1/(alpha - beta) after the loop.
 __device__ __forceinline__ void wave_lds_sync() {
   __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
   __builtin_amdgcn_wave_barrier();
@@ -134,6 +136,7 @@ __global__ void __launch_bounds__(NW * 64) panel_kernel(float* __restrict__ H, i
     }
   }
   float* xq = xs + q * XS;
+  float my_inv = 0.0f;  // 1 / (alpha - beta) of this lane's column, once factored
 
   for (int j = 0; j < w; ++j) {
     const int par = j & 1;
@@ -191,29 +194,39 @@ __global__ void __launch_bounds__(NW * 64) panel_kernel(float* __restrict__ H, i
     const float sigma = readlane(tot, j);
     const float alpha = readlane(rowt, j);
     const Reflector rf = make_reflector(alpha, sigma);
+    // Finished columns c < j keep their unscaled x_c (v_c = x_c * inv_c is
+    // applied after the loop), so here z_c = inv_c * (v_c^T v).
     const float z = fmaf(tot, rf.inv, rowt);
     const float s = (c > j && c < w) ? rf.tau * z : 0.0f;
     if (wave == 0 && qw == 0) {
-      ys[c][j] = z;
+      ys[c][j] = (c < j) ? my_inv * z : z;
       if (c == j) taus[j] = rf.tau;
     }
-    // c == j: a <- (a - x) + x*inv  (exactly x*inv on rows > j, a elsewhere)
-    // c != j: a <- a + x * (-s*inv)
-    const bool isj = (c == j);
-    const float alp = isj ? rf.inv : -s * rf.inv;
-    const float bet = isj ? -1.0f : 0.0f;
+    if (c == j) my_inv = rf.inv;
+    // a_r[c] -= tau z_c v_r with v_r = x_r * inv  (s == 0 on columns c <= j)
+    const float alp = -s * rf.inv;
 #pragma unroll
     for (int i = 0; i < R; i += 4) {
       const f32x4 x = *reinterpret_cast<const f32x4*>(xq + i);
 #pragma unroll
-      for (int u = 0; u < 4; ++u) A_(i + u) = fmaf(x[u], alp, fmaf(bet, x[u], A_(i + u)));
+      for (int u = 0; u < 4; ++u) A_(i + u) = fmaf(x[u], alp, A_(i + u));
     }
     if (q == 0) {
       const float aj = av[0][ju];
-      av[0][ju] = isj ? rf.beta : aj - s;
+      av[0][ju] = (c == j) ? rf.beta : aj - s;
     }
     // the next step's publish reuses xq: keep this step's reads ahead of it
     wave_lds_sync();
+  }
+
+  // v_c = x_c * inv_c below the diagonal (opaque row base: the masks are not
+  // hoisted above the loop, where they would stay live in registers)
+  {
+    int r0v = row0, cv = c;
+    asm volatile("" : "+v"(r0v), "+v"(cv));
+#pragma unroll
+    for (int i = 0; i < R; ++i)
+      if (r0v + i > cv) A_(i) *= my_inv;
   }
 
 #pragma unroll
