@@ -143,3 +143,28 @@ def test_benchmark_workloads_match_geqrf(cuda, name, idx, limit):
     h, tau = run_gpu(a, cuda)
     ag = assert_parity(a, h, tau)
     _say(f"  {ag.message()}")
+
+
+def test_forced_error_surfaces_as_exception(cuda):
+    _say("[error hook]")
+    import fastqr
+
+    fastqr.cdll().fastqr_debug_force_error(-99)
+    with pytest.raises(fastqr.FastQRError) as exc:
+        custom_kernel(torch.randn((2, 8, 8), device=cuda))
+    assert exc.value.code == -99
+
+
+@pytest.mark.parametrize("n", [48, 200])
+def test_geqrf_into_padded_leading_dimension(cuda, n):
+    _say(f"[padded H] n={n}")
+    import fastqr
+
+    a = gaussian(3, n, 500 + n)
+    h_ref, tau_ref = run_gpu(a, cuda)
+    store = torch.full((3, n + 8, n), float("nan"), device=cuda)  # leading dimension n + 8
+    h = store.as_strided((3, n, n), ((n + 8) * n, 1, n + 8))
+    tau = torch.empty((3, n), device=cuda)
+    fastqr.geqrf_into(a.to(cuda), h, tau)
+    torch.cuda.synchronize()
+    assert torch.equal(h.cpu(), h_ref) and torch.equal(tau.cpu(), tau_ref)

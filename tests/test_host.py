@@ -1,0 +1,206 @@
+"""Host-side checks that need no GPU: the C ABI library, argument validation,
+the Python mirror of the reference interface, workload generators, bench CLI.
+
+Nothing here launches a kernel: every fastqr_geqrf_f32 call below is rejected
+by validation (or is an empty batch) before any HIP call is made.
+"""
+import ctypes
+import inspect
+import os
+import re
+import subprocess
+import sys
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+import fastqr
+from fastqr import _lib, inputs, workspace
+
+ROOT = Path(__file__).resolve().parents[1]
+HEADER = ROOT / "include" / "fastqr.h"
+
+
+def header_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(fastqr_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_exports_every_declared_symbol():
+    lib = ctypes.CDLL(str(_lib.LIB_PATH))
+    declared = header_functions()
+    assert declared, "no functions parsed from include/fastqr.h"
+    for name in declared:
+        assert hasattr(lib, name), f"{name} declared in fastqr.h but not exported"
+    assert sorted(_lib.EXPORTED_SYMBOLS) == declared
+
+
+def test_version_and_path_names():
+    lib = fastqr.cdll()
+    assert lib.fastqr_version() == 1
+    assert lib.fastqr_path_name(1) == b"wave64"
+    assert lib.fastqr_path_name(64) == b"wave64"
+    assert lib.fastqr_path_name(65) == b"blocked"
+    assert fastqr.ext().version() == 1
+    assert fastqr.path_for(4096) == "blocked"
+
+
+def test_workspace_bytes():
+    lib = fastqr.cdll()
+    assert lib.fastqr_workspace_bytes(20, 32) == 0  # wave path needs none
+    assert lib.fastqr_workspace_bytes(0, 512) == 0
+    small = lib.fastqr_workspace_bytes(1, 512)
+    assert small > 0 and small % 256 == 0
+    assert lib.fastqr_workspace_bytes(640, 512) >= 640 * small - 255
+
+
+def _call(lib, A=8, b=2, n=100, a_s=(None,), H=16, h_s=None, tau=32, t_s=None, ws=64, ws_bytes=1 << 20):
+    a_s0, a_s1, a_s2 = (n * n, n, 1) if a_s == (None,) else a_s
+    h_s0, h_s1, h_s2 = (n * n, 1, n) if h_s is None else h_s
+    t_s0, t_s1 = (n, 1) if t_s is None else t_s
+    # fake, never-dereferenced "device" addresses far apart (validation only)
+    base = 1 << 40
+    return lib.fastqr_geqrf_f32(base * A if A else None, b, n, a_s0, a_s1, a_s2, base * H if H else None, h_s0,
+                                h_s1, h_s2, base * tau if tau else None, t_s0, t_s1, base * ws if ws else None,
+                                ws_bytes, None)
+
+
+def test_argument_validation_returns_codes_without_launching():
+    lib = fastqr.cdll()
+    assert _call(lib, b=0) == _lib.FASTQR_OK  # empty batch: nothing to do
+    assert _call(lib, n=0) == _lib.FASTQR_OK
+    assert _call(lib, n=-3) == _lib.FASTQR_EINVAL
+    assert _call(lib, A=0) == _lib.FASTQR_EINVAL
+    assert b"non-null" in lib.fastqr_last_error()
+    assert _call(lib, n=9000) == _lib.FASTQR_EINVAL
+    # blocked path needs contiguous columns of H
+    assert _call(lib, n=100, h_s=(10000, 100, 1)) == _lib.FASTQR_ELAYOUT
+    assert b"contiguous columns" in lib.fastqr_last_error()
+    assert _call(lib, n=100, ws_bytes=16) == _lib.FASTQR_EWORKSPACE
+    assert _call(lib, n=100, ws=0) == _lib.FASTQR_EWORKSPACE
+    # A and H overlapping with different layouts
+    assert _call(lib, n=100, A=16, a_s=(10000, 100, 1)) == _lib.FASTQR_EOVERLAP
+    assert _call(lib, n=32, A=16, a_s=(1024, 32, 1)) == _lib.FASTQR_EOVERLAP
+    assert _call(lib, t_s=(100, 0)) == _lib.FASTQR_EINVAL
+    assert _call(lib, a_s=(-1, 100, 1)) == _lib.FASTQR_EINVAL
+
+
+def test_forced_error_hook_round_trip():
+    lib = fastqr.cdll()
+    lib.fastqr_debug_force_error(-99)
+    assert _call(lib) == -99
+    assert b"forced error" in lib.fastqr_last_error()
+    # the hook fires once; the next (invalid) call reports its own error
+    assert _call(lib, A=0) == _lib.FASTQR_EINVAL
+
+
+def test_profile_hooks_without_work():
+    _lib.profile_enable(True)
+    stats = _lib.profile_collect()
+    _lib.profile_enable(False)
+    assert set(stats) == set(_lib.PROFILE_KINDS)
+    assert all(v["launches"] == 0 for v in stats.values())
+    assert fastqr.cdll().fastqr_profile_collect(7, None, None, None, None) == _lib.FASTQR_EINVAL
+
+
+def test_custom_kernel_interface_matches_reference():
+    # official/submission.py:5-6 / tests/test_case_files.py:64-69: exactly custom_kernel(data)
+    params = list(inspect.signature(fastqr.custom_kernel).parameters)
+    assert params == ["data"]
+    sys.path.insert(0, str(ROOT / "fast-qr_amd"))
+    import submission  # noqa: F401  (the drop-in module)
+
+    assert submission.custom_kernel is fastqr.custom_kernel
+
+
+def test_custom_kernel_rejects_bad_inputs_loudly():
+    with pytest.raises(TypeError):
+        fastqr.custom_kernel(torch.zeros((2, 4, 4), dtype=torch.float64))
+    with pytest.raises(ValueError):
+        fastqr.custom_kernel(torch.zeros((2, 4, 5)))
+    with pytest.raises(ValueError):
+        fastqr.custom_kernel(torch.zeros((2, 4, 4)))  # CPU tensor: no silent fallback
+    with pytest.raises(TypeError):
+        fastqr.custom_kernel(np.zeros((2, 4, 4), np.float32))
+
+
+def test_column_major_allocator_layout():
+    # tests/test_qr_smoke.py:8088-8095 of the reference
+    data = torch.empty((3, 16, 16))
+    h = fastqr.allocate_column_major_H(3, 16, data)
+    assert h.shape == (3, 16, 16) and h.dtype == torch.float32 and h.stride() == (256, 1, 16)
+    tau = fastqr.allocate_tau(3, 16, data)
+    assert tau.shape == (3, 16) and tau.stride() == (16, 1)
+
+
+def test_output_workspace_cache_is_per_input(monkeypatch):
+    # tests/test_qr_smoke.py:8097-8143 of the reference
+    workspace.clear()
+    monkeypatch.setenv("FASTQR_OUTPUT_WORKSPACE_CACHE", "1")
+    data_a = torch.empty((3, 16, 16))
+    data_b = torch.empty((3, 16, 16))
+    h_a = fastqr.allocate_column_major_H(3, 16, data_a)
+    h_a.fill_(1.0)
+    h_a_again = fastqr.allocate_column_major_H(3, 16, data_a)
+    h_b = fastqr.allocate_column_major_H(3, 16, data_b)
+    assert h_a_again.data_ptr() == h_a.data_ptr()
+    assert h_b.data_ptr() != h_a.data_ptr()
+    tau_a = fastqr.allocate_tau(3, 16, data_a)
+    tau_a.fill_(7.0)
+    tau_zero = fastqr.allocate_tau(3, 16, data_a, zero=True)
+    assert tau_zero.data_ptr() == tau_a.data_ptr() and not tau_zero.any()
+    h2, t2 = fastqr.allocate_h_tau(3, 16, data_b)
+    assert h2.data_ptr() == h_b.data_ptr() and t2.data_ptr() != tau_a.data_ptr()
+    # a freed input drops its cache entries
+    key_count = len(workspace._OUTPUT_CACHE)
+    del data_b, h_b, h2, t2
+    import gc
+
+    gc.collect()
+    assert len(workspace._OUTPUT_CACHE) < key_count
+    monkeypatch.setenv("FASTQR_OUTPUT_WORKSPACE_CACHE", "0")
+    assert fastqr.allocate_column_major_H(3, 16, data_a).data_ptr() != h_a.data_ptr()
+
+
+def test_workload_generators_are_seeded_and_structured():
+    s = inputs.Shape(8, 64, "c3mixed", 11)
+    a1, a2 = inputs.generate(s), inputs.generate(s)
+    assert torch.equal(a1, a2) and a1.dtype == torch.float32 and a1.is_contiguous()
+    labels = inputs.structure_labels(s)
+    assert labels.count("rankdef") == 2 and labels.count("clustered") == 2 and labels.count("dense") == 4
+    for i, lab in enumerate(labels):
+        sv = torch.linalg.svdvals(a1[i].double())
+        if lab == "rankdef":
+            assert sv[31] > 0.99 and sv[32] < 1e-5
+        elif lab == "clustered":
+            assert sv[31] > 0.99 and 5e-7 < sv[32] < 2e-6
+    s4 = inputs.Shape(8, 300, "c4mixed", 12)
+    a4 = inputs.generate(s4)
+    for i, lab in enumerate(inputs.structure_labels(s4)):
+        if lab == "nearrank":
+            sv = torch.linalg.svdvals(a4[i].double())
+            assert sv[300 - 257] > 0.99 and sv[300 - 256] < 2e-7
+    assert inputs.flops(2, 3) == pytest.approx(2 * 4 * 27 / 3)
+    assert inputs.bytes_moved(1, 4) == 8 * 16 + 16
+
+
+def test_bench_input_count_matches_official_formula():
+    # official/eval.py:167-175; tests/test_case_files.py:731-736 of the reference
+    sys.path.insert(0, str(ROOT))
+    import bench
+
+    assert bench.count_for(20, 32) == 50
+    assert bench.count_for(640, 512) == 1
+    assert bench.count_for(60, 1024) == 1
+    assert bench.count_for(2, 4096) == 2
+
+
+def test_bench_refuses_multi_gpu():
+    env = dict(os.environ)
+    r = subprocess.run([sys.executable, str(ROOT / "bench.py"), "--gpus", "2"], capture_output=True, text=True,
+                       env=env, timeout=120)
+    assert r.returncode == 2
+    assert "one GPU" in r.stderr

@@ -1,0 +1,197 @@
+"""Pins the CPU oracle (oracle/hhqr.c, oracle/checker.py) before it is trusted.
+
+Checks, each chosen so a plausible mistake (sign, index, transposed operand,
+dropped term) fails at least one:
+  * golden vectors from torch.geqrf (the reference's own path) and scipy's
+    LAPACK sgeqrf, tests/golden/*.npz;
+  * closed forms: the slarfg reflector, n = 1, the 2x2 factorisation;
+  * known answers: upper-triangular input -> tau == 0 and H == A bit-exact
+    (tests/test_qr_smoke.py:8078-8085 of the reference), zero matrix, a column
+    already zero below the diagonal;
+  * invariants: Q R = A and Q^T Q = I through the official checker
+    (official/reference.py:182-266) and its diagnostics bounds
+    (tests/test_qr_smoke.py:192-200);
+  * compact WY: I - V T V^T equals the product of the reflectors, and the
+    blocked factorisation equals the unblocked one within 2e-5
+    (the pattern of tests/test_qr_smoke.py:261-276);
+  * planted mistakes in the oracle (mutation flags) are caught.
+"""
+import math
+from pathlib import Path
+
+import numpy as np
+import pytest
+import torch
+
+from oracle import checker, oracle
+
+GOLDEN = Path(__file__).resolve().parent / "golden"
+
+
+def load(name):
+    with np.load(GOLDEN / f"{name}.npz") as z:
+        return {k: z[k] for k in z.files}
+
+
+GOLDEN_CASES = ["gauss_20x32", "gauss_6x1", "gauss_6x2", "gauss_6x3", "gauss_6x4", "gauss_6x5", "gauss_6x8",
+                "rankdef_4x8", "colscaled_4x8", "upper_4x8"]
+
+
+@pytest.mark.parametrize("name", GOLDEN_CASES)
+def test_golden_lapack_vectors_agree_with_each_other(name):
+    g = load(name)
+    # torch.geqrf (MKL) and scipy sgeqrf are two LAPACKs: they agree on R diag / tau
+    ag = checker.rdiag_tau_agreement(g["a"], g["h_scipy"], g["tau_scipy"], g["h"], g["tau"])
+    assert ag.ok, ag.message()
+
+
+@pytest.mark.parametrize("name", GOLDEN_CASES)
+def test_restated_oracle_matches_golden(name):
+    g = load(name)
+    h, tau = oracle.geqrf_restated(g["a"])
+    ok, msg = checker.official_check(g["a"], h, tau)
+    assert ok, msg
+    ag = checker.rdiag_tau_agreement(g["a"], h, tau, g["h"], g["tau"])
+    assert ag.ok, ag.message()
+    # well-conditioned columns: the whole compact factor matches LAPACK closely
+    if name.startswith("gauss"):
+        np.testing.assert_allclose(h, g["h"], rtol=0, atol=2e-4 * np.abs(g["h"]).max())
+        np.testing.assert_allclose(tau, g["tau"], rtol=0, atol=2e-5)
+
+
+def test_reflector_closed_forms():
+    # slarfg: beta = -sign(alpha) ||(alpha, x)||, tau = (beta - alpha) / beta
+    beta, tau, denom, active = oracle.reflector(3.0, 16.0)
+    assert active and beta == -5.0 and tau == pytest.approx(1.6) and denom == 8.0
+    beta, tau, denom, active = oracle.reflector(-3.0, 16.0)
+    assert active and beta == 5.0 and tau == pytest.approx(1.6) and denom == -8.0
+    beta, tau, denom, active = oracle.reflector(0.0, 4.0)  # alpha = +0 takes beta <= 0
+    assert active and beta == -2.0 and tau == 1.0 and denom == 2.0
+    beta, tau, denom, active = oracle.reflector(-7.0, 0.0)  # sigma == 0: identity, beta = alpha
+    assert not active and beta == -7.0 and tau == 0.0
+
+
+def test_n1_is_identity_factorisation():
+    a = np.array([[[2.5]], [[-1.0]], [[0.0]]], dtype=np.float32)
+    h, tau = oracle.geqrf_restated(a)
+    assert np.array_equal(h, a) and np.array_equal(tau, np.zeros((3, 1), np.float32))
+
+
+def test_2x2_closed_form():
+    a = np.array([[[3.0, 1.0], [4.0, 2.0]]], dtype=np.float32)
+    h, tau = oracle.geqrf_restated(a)
+    # alpha=3, x=4: beta=-5, tau=1.6, v1=4/8=0.5 ; R01 = 1 - tau*(1 + 0.5*2) = -2.2 ;
+    # R11 = 2 - tau*0.5*(1 + 0.5*2) = 0.4 ; the last column has no reflector.
+    np.testing.assert_allclose(h[0], [[-5.0, -2.2], [0.5, 0.4]], rtol=1e-6)
+    np.testing.assert_allclose(tau[0], [1.6, 0.0], rtol=1e-6)
+    ref_h, ref_tau = torch.geqrf(torch.from_numpy(a))
+    np.testing.assert_allclose(h, ref_h.numpy(), rtol=1e-6)
+    np.testing.assert_allclose(tau, ref_tau.numpy(), rtol=1e-6)
+
+
+def test_upper_triangular_input_known_answer():
+    g = load("upper_4x8")
+    h, tau = oracle.geqrf_restated(g["a"])
+    assert np.array_equal(tau, np.zeros_like(tau))
+    assert np.array_equal(h, g["a"])
+    assert np.array_equal(g["tau"], np.zeros_like(g["tau"]))  # LAPACK agrees
+
+
+def test_zero_matrix_and_zero_subcolumn():
+    h, tau = oracle.geqrf_restated(np.zeros((2, 5, 5), np.float32))
+    assert not h.any() and not tau.any()
+    a = np.random.default_rng(0).standard_normal((1, 5, 5)).astype(np.float32)
+    a[0, 1:, 0] = 0.0  # column 0 already reduced
+    h, tau = oracle.geqrf_restated(a)
+    assert tau[0, 0] == 0.0 and h[0, 0, 0] == a[0, 0, 0]
+
+
+def test_fp32_restatement_close_to_fp64_restatement():
+    g = load("gauss_20x32")
+    h32, t32 = oracle.geqrf_restated(g["a"])
+    h64, t64 = oracle.geqrf_restated_f64(g["a"])
+    ag = checker.rdiag_tau_agreement(g["a"], h32, t32, h64.astype(np.float32), t64.astype(np.float32))
+    assert ag.ok, ag.message()
+
+
+def _reflector_product(v_block, tau):
+    m, nb = v_block.shape
+    q = np.eye(m)
+    for j in range(nb):
+        v = np.zeros(m)
+        v[j] = 1.0
+        v[j + 1 :] = v_block[j + 1 :, j]
+        q = q @ (np.eye(m) - tau[j] * np.outer(v, v))
+    return q
+
+
+def test_compact_wy_equals_reflector_product():
+    g = load("gauss_6x8")
+    h, tau = oracle.geqrf_restated(g["a"])
+    for b in range(3):
+        v_block = h[b].astype(np.float64)
+        t = oracle.larft(h[b], tau[b]).astype(np.float64)
+        m, nb = v_block.shape
+        v = np.tril(v_block, -1) + np.eye(m, nb)
+        wy = np.eye(m) - v @ t @ v.T
+        np.testing.assert_allclose(wy, _reflector_product(v_block, tau[b]), atol=2e-6)
+        assert np.allclose(np.tril(t, -1), 0.0)  # T is upper triangular
+        np.testing.assert_allclose(np.diag(t), tau[b], rtol=1e-6)
+
+
+@pytest.mark.parametrize("nb", [1, 3, 5, 8, 32])
+def test_blocked_restatement_matches_unblocked(nb):
+    # tools/blocked_qr_reference.py panel loop; tests/test_qr_smoke.py:203-214, 261-276
+    a = torch.randn((3, 40, 40), generator=torch.Generator().manual_seed(nb)).numpy()
+    hb, tb = oracle.geqrf_restated_blocked(a, nb)
+    hu, tu = oracle.geqrf_restated(a)
+    np.testing.assert_allclose(hb, hu, rtol=2e-5, atol=2e-5)
+    np.testing.assert_allclose(tb, tu, rtol=2e-5, atol=2e-5)
+    ok, msg = checker.official_check(a, hb, tb)
+    assert ok, msg
+
+
+def test_geqrf_passes_checker_with_diagnostic_bounds():
+    g = load("gauss_20x32")
+    ok, msg = checker.official_check(g["a"], g["h"], g["tau"])
+    assert ok, msg
+    fields = dict(kv.split("=") for kv in msg.split("; "))
+    assert float(fields["scaled_factor_residual"]) < 20.0
+    assert float(fields["scaled_orthogonality_residual"]) < 100.0
+    assert checker.frobenius_gates(g["a"], g["h"], g["tau"]).ok
+
+
+@pytest.mark.parametrize("mutation,kind", [(1, "agreement"), (2, "official"), (3, "official")])
+def test_planted_mistakes_are_caught(mutation, kind):
+    a = torch.randn((4, 24, 24), generator=torch.Generator().manual_seed(7)).numpy()
+    if mutation == 1:
+        # flipped beta sign: still a valid QR, but not LAPACK's factorisation
+        h, tau = oracle.geqrf_restated(a, mutation=1)
+        ref_h, ref_tau = torch.geqrf(torch.from_numpy(a))
+        assert not checker.rdiag_tau_agreement(a, h, tau, ref_h, ref_tau).ok
+    else:
+        # T in place of T^T, or a dropped unit diagonal, in the trailing update
+        h, tau = oracle.geqrf_restated_blocked(a, 4, mutation=mutation)
+        ok, _ = checker.official_check(a, h, tau)
+        assert not ok
+        assert not checker.frobenius_gates(a, h, tau).ok
+
+
+def test_checker_rejects_bad_outputs():
+    g = load("gauss_6x8")
+    a, h, tau = g["a"], g["h"].copy(), g["tau"].copy()
+    assert not checker.official_check(a, h[:, :, :7], tau)[0]
+    bad = tau.copy()
+    bad[0, 0] = np.nan
+    assert not checker.official_check(a, h, bad)[0]
+    h2 = h.copy()
+    h2[1, 3, 2] += 0.5  # corrupt a reflector entry
+    assert not checker.official_check(a, h2, tau)[0]
+
+
+def test_agreement_floor_masks_rank_deficient_tail_only():
+    g = load("rankdef_4x8")
+    rep = checker.rdiag_tau_agreement(g["a"], g["h_scipy"], g["tau_scipy"], g["h"], g["tau"])
+    assert rep.ok and rep.masked >= 4 * 2  # the two copied columns per matrix are noise
+    assert rep.compared >= 4 * 5
+    assert math.isfinite(rep.rdiag_rel_max)
