@@ -20,6 +20,9 @@ int panel_width_for(int m);
 hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float* tau, int64_t ts0,
                         int64_t ts1, float* Tws, int n, int k0, int nb, int m_cap, int slot, bool vec,
                         hipStream_t stream);
+// 32-column panel (m <= 2048 rows), qr_panel.hip.
+hipError_t launch_panel32(float* H, int64_t batch, int64_t hs0, int64_t ldh, float* tau, int64_t ts0, int64_t ts1,
+                          float* Tws, int n, int k0, int slot, hipStream_t stream);
 // Apply nwy compact-WY transforms (panels k0 + i*nb, T slots slot0 + i) to
 // columns [c_begin, c_end), rows [k0, n).
 hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n,

@@ -585,6 +585,7 @@ hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float
       hipLaunchKernelGGL((panel_kernel<NB, NW, R, false>), grid, dim3(NW * 64), 0, stream, H, hs0, ldh,    \
                          tau, ts0, ts1, Tws, n, k0, slot);                                                \
   } while (0)
+  if (nb == 32 && m <= 2048) return launch_panel32(H, batch, hs0, ldh, tau, ts0, ts1, Tws, n, k0, slot, stream);
   if (nb == 32) {
     if (m <= 128) {
       FASTQR_PANEL(32, 2, 32);
