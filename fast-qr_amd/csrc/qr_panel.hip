@@ -10,8 +10,8 @@
 // (panel columns 0-15) and of block 1 (columns 16-31).  Wave w owns tiles
 // w, w+NW, ...  A 16-lane DPP row therefore holds 4 rows of all 16 columns of
 // a block, so the pivot column j of a block is broadcast to its row with the
-// row_newbcast:j DPP modifier, fused into the FMAs: no LDS traffic for the
-// Householder vector.
+// row_newbcast:j DPP modifier fused into the FMAs (v_fmac_f32_dpp): no LDS
+// traffic and no extra moves for the Householder vector.
 //
 // Block 0 is factored column by column (one reduction per column, as the
 // wider kernel in qr_blocked.hip); its compact-WY transform is then applied
@@ -29,10 +29,36 @@ namespace fastqr {
 
 typedef float f32x4v __attribute__((ext_vector_type(4)));
 
+// The compiler's DPP combiner does not fold a row_newbcast move into an FMA, so
+// the two fused forms the column loop needs are written out.  Each block opens
+// with "s_nop 1": the two wait states a DPP read needs after a VALU write of its
+// source register, which the compiler's hazard tracking cannot see across asm.
+// row_newbcast:J reads lane J of each 16-lane row; every lane is written.
+
+// g0 += b(x0) y0 + b(x2) y2,  g1 += b(x1) y1 + b(x3) y3,  b = row_newbcast:J
 template <int J>
-__device__ __forceinline__ float row_bcast(float v) {
-  // row_newbcast:J — lane J of each 16-lane row to the whole row
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + J, 0xF, 0xF, true));
+__device__ __forceinline__ void bcast_dot4(float& g0, float& g1, f32x4v x, f32x4v y) {
+  asm("s_nop 1\n\t"
+      "v_fmac_f32_dpp %0, %2, %6 row_newbcast:%c10 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %3, %7 row_newbcast:%c10 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %0, %4, %8 row_newbcast:%c10 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %5, %9 row_newbcast:%c10 row_mask:0xf bank_mask:0xf"
+      : "+v"(g0), "+v"(g1)
+      : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(y[0]), "v"(y[1]), "v"(y[2]), "v"(y[3]), "i"(J));
+}
+
+// x_i += b(x_i) a_i,  b = row_newbcast:J
+template <int J>
+__device__ __forceinline__ void bcast_axpy4(f32x4v& x, float a0, float a1, float a2, float a3) {
+  float x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
+  asm("s_nop 1\n\t"
+      "v_fmac_f32_dpp %0, %0, %4 row_newbcast:%c8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %1, %5 row_newbcast:%c8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %2, %2, %6 row_newbcast:%c8 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %3, %3, %7 row_newbcast:%c8 row_mask:0xf bank_mask:0xf"
+      : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3)
+      : "v"(a0), "v"(a1), "v"(a2), "v"(a3), "i"(J));
+  x = f32x4v{x0, x1, x2, x3};
 }
 
 template <class F, int... I>
@@ -98,20 +124,17 @@ __global__ void __launch_bounds__(NW * 64) panel32_kernel(float* __restrict__ H,
           if (JG >= w) return;
           constexpr int PAR = JJ & 1;
           // partial  sum_{r > JG} x_r a_r[cn]  over this lane's rows
+          // (rows <= JG lie only in the first tile of each wave; they are masked there)
+          const int rb0 = 16 * wave + 4 * kq;
           float g0 = 0.0f, g1 = 0.0f;
+          {
+            f32x4v y;
 #pragma unroll
-          for (int t = 0; t < TPW; ++t) {
-            const int rbase = 16 * (wave + NW * t) + 4 * kq;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              float x = row_bcast<JJ>(X[BLK][t][i]);
-              if (t == 0) x = (rbase + i > JG) ? x : 0.0f;  // only the first tiles reach row JG
-              if (i & 1)
-                g1 = fmaf(x, X[BLK][t][i], g1);
-              else
-                g0 = fmaf(x, X[BLK][t][i], g0);
-            }
+            for (int i = 0; i < 4; ++i) y[i] = (rb0 + i > JG) ? X[BLK][0][i] : 0.0f;
+            bcast_dot4<JJ>(g0, g1, X[BLK][0], y);
           }
+#pragma unroll
+          for (int t = 1; t < TPW; ++t) bcast_dot4<JJ>(g0, g1, X[BLK][t], X[BLK][t]);
           float g = g0 + g1;
           // row JG of my column: tile BLK, row 4*(JJ/4) + JJ%4 of it
           constexpr int T_OWN = BLK / NW;
@@ -144,16 +167,10 @@ __global__ void __launch_bounds__(NW * 64) panel32_kernel(float* __restrict__ H,
           }
           if (cn == JJ) my_inv[BLK] = rf.inv;
           const float alp = -s * rf.inv;
+          bcast_axpy4<JJ>(X[BLK][0], (rb0 > JG) ? alp : 0.0f, (rb0 + 1 > JG) ? alp : 0.0f,
+                          (rb0 + 2 > JG) ? alp : 0.0f, (rb0 + 3 > JG) ? alp : 0.0f);
 #pragma unroll
-          for (int t = 0; t < TPW; ++t) {
-            const int rbase = 16 * (wave + NW * t) + 4 * kq;
-#pragma unroll
-            for (int i = 0; i < 4; ++i) {
-              float x = row_bcast<JJ>(X[BLK][t][i]);
-              if (t == 0) x = (rbase + i > JG) ? x : 0.0f;
-              X[BLK][t][i] = fmaf(x, alp, X[BLK][t][i]);
-            }
-          }
+          for (int t = 1; t < TPW; ++t) bcast_axpy4<JJ>(X[BLK][t], alp, alp, alp, alp);
           if (wave == BLK % NW && kq == JJ / 4) {
             const float a = X[BLK][T_OWN][JJ & 3];
             X[BLK][T_OWN][JJ & 3] = (cn == JJ) ? rf.beta : a - s;
