@@ -76,6 +76,27 @@ __device__ __forceinline__ float xor32_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// v(lane) + v(lane ^ 16): the two results of one v_permlane16_swap(v, v) are
+// {v_l, v_(l^16)} in some order in every lane.
+__device__ __forceinline__ float xor16_sum(float v) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+// Reflector without branches (alpha, sigma wave-uniform): the same values as
+// make_reflector, selected instead of branched on so a column step has no
+// scalar branch.
+__device__ __forceinline__ Reflector make_reflector_sel(float alpha, float sigma) {
+  const float nrm = __builtin_amdgcn_sqrtf(fmaf(alpha, alpha, sigma));
+  const float bt = (alpha >= 0.0f) ? -nrm : nrm;
+  const bool act = sigma > 0.0f;
+  Reflector r;
+  r.tau = act ? (bt - alpha) * __builtin_amdgcn_rcpf(bt) : 0.0f;
+  r.inv = act ? __builtin_amdgcn_rcpf(alpha - bt) : 0.0f;
+  r.beta = act ? bt : alpha;
+  return r;
+}
+
 // Sum over all 64 lanes, result in every lane.
 __device__ __forceinline__ float wave_sum(float v) {
   v = xor32_sum(v);

@@ -33,7 +33,7 @@ int hip_fail(hipError_t e, const char* what) {
   return fail((int)e, "%s: %s", what, hipGetErrorString(e));
 }
 
-constexpr int64_t kMaxN = 8192;
+constexpr int64_t kMaxN = 4096;
 constexpr int kWaveMaxN = 64;
 
 bool ranges_overlap(const float* a, int64_t a_elems, const float* b, int64_t b_elems) {

@@ -14,15 +14,18 @@ hipError_t launch_qr_wave(const float* A, int64_t batch, int n, int64_t as0, int
 // Blocked path (qr_blocked.hip).
 hipError_t launch_copy_colmajor(const float* A, int64_t batch, int n, int64_t as0, int64_t as1, int64_t as2,
                                 float* H, int64_t hs0, int64_t ldh, hipStream_t stream);
+// Panel width (32, or 16 above 2048 rows) and the tallest panel supported (qr_panel.hip).
 int panel_width_for(int m);
+int panel_max_rows();
 // Panel of width nb at column k0, template sized for m_cap >= n - k0 rows;
 // its T factor goes to workspace slot `slot`.
+// Explicit (waves, tiles per wave) variant of launch_panel, for tuning.
+hipError_t launch_panel_cfg(int nw, int tpw, float* H, int64_t batch, int64_t hs0, int64_t ldh, float* tau,
+                            int64_t ts0, int64_t ts1, float* Tws, int n, int k0, int nb, int slot, bool vec,
+                            hipStream_t stream);
 hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float* tau, int64_t ts0,
                         int64_t ts1, float* Tws, int n, int k0, int nb, int m_cap, int slot, bool vec,
                         hipStream_t stream);
-// 32-column panel (m <= 2048 rows), qr_panel.hip.
-hipError_t launch_panel32(float* H, int64_t batch, int64_t hs0, int64_t ldh, float* tau, int64_t ts0, int64_t ts1,
-                          float* Tws, int n, int k0, int slot, hipStream_t stream);
 // Apply nwy compact-WY transforms (panels k0 + i*nb, T slots slot0 + i) to
 // columns [c_begin, c_end), rows [k0, n).
 hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n,

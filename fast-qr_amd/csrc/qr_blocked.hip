@@ -1,27 +1,16 @@
-// qr_blocked.hip — blocked compact-WY Householder QR for n > 64.
+// qr_blocked.hip — blocked compact-WY Householder QR for n > 64: the copy of A
+// into H and the trailing update.  The panel factorisation is in qr_panel.hip.
 //
 // Reference counterpart: geqrf{n}_blocked_cuda_impl and its kernels,
-// submissions/candidate.py:2100-2161 (copy), 2404-2505 (panel factor),
-// 2507-2716 (trailing update), 2718-2933 (host loop), restricted to the full
-// fp32 factorisation (factor_cols = n, no tail projection, no repair).
+// submissions/candidate.py:2100-2161 (copy), 2507-2716 (trailing update),
+// restricted to the full fp32 factorisation (factor_cols = n, no tail
+// projection, no repair).
 //
-// Per panel [k0, k0 + w) of width w <= NB:
-//   panel_kernel   one workgroup per matrix.  The (n-k0) x w panel lives in
-//                  VGPRs, each lane owning a run of rows of one column.  Each
-//                  column step does ONE reduction per column c,
-//                      tot_c = sum_{r>j} x_r * a_r[c]            (all c)
-//                  which yields sigma (c == j), the Gram row used for the
-//                  update of later columns (c > j), and v_c^T x used for the
-//                  T factor (c < j).  The reference needs a reduction for
-//                  sigma plus one per chunk of columns (submissions/candidate.py:2437-2498)
-//                  and recomputes T in every trailing CTA (2544-2584); here T
-//                  is built once per panel (slarft recurrence) and stored in
-//                  the workspace.
-//   update_kernel  grid = (32-column strips, batch).  A2 <- A2 - V (T^T (V^T A2))
-//                  with v_mfma_f32_32x32x2f32.  A2 tiles are held in the MFMA
-//                  accumulator layout and reused directly as the B operand of
-//                  V^T A2 by permuting the contraction index (any order of
-//                  the row sum is valid), so no register shuffles are needed.
+//   wy_update_kernel  grid = (32-column strips, batch).  A2 <- A2 - V (T^T (V^T A2))
+//                     with v_mfma_f32_32x32x2f32.  A2 tiles are held in the MFMA
+//                     accumulator layout and reused directly as the B operand of
+//                     V^T A2 by permuting the contraction index (any order of
+//                     the row sum is valid), so no register shuffles are needed.
 #include "device.hpp"
 #include "kernels.hpp"
 
@@ -64,267 +53,8 @@ __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __re
 }
 
 // ---------------------------------------------------------------------------
-// Panel factorisation
-// ---------------------------------------------------------------------------
-// Layout: lane (chunk q, column c) holds rows [q*R, q*R + R) of panel column c
-// in R VGPRs (an ext_vector so a uniform row index lowers to s_set_gpr_idx).
-// A wave holds CPW = 64/NB chunks; the workgroup NW*CPW chunks.  At step j:
-//   1. the lanes of column j publish their (masked) rows of column j to a
-//      per-chunk LDS slot, read back by the lanes of the same chunk (same wave:
-//      no workgroup barrier);
-//   2. lane (q, c) forms the partial  sum_{r>j, r in q} x_r a_r[c]  and the
-//      chunk's copy of row j; partials are summed over the chunks of the wave
-//      with xor shuffles, then over waves through LDS (one barrier);
-//   3. every lane derives the reflector (alpha = row j of column j, sigma =
-//      total of column j) and, for its column c,
-//        z_c = a_j[c] + tot_c / (alpha - beta)
-//      which is v^T a_c for c > j (update scale) and, times 1/(alpha_c -
-//      beta_c), v_c^T v for c < j (the slarft inputs, kept in LDS for the T
-//      factor built after the loop);
-//   4. updates its rows  a_r[c] -= tau z_c v_r  and row j.
-// A finished column keeps its unscaled x below the diagonal (no per-step
-// scaling pass); it is multiplied by its 1/(alpha - beta) after the loop.
-__device__ __forceinline__ void wave_lds_sync() {
-  __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-  __builtin_amdgcn_wave_barrier();
-  __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-}
-
-template <int NB, int NW, int R, bool VEC>
-__global__ void __launch_bounds__(NW * 64) panel_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh,
-                                                        float* __restrict__ tau, int64_t ts0, int64_t ts1,
-                                                        float* __restrict__ Tws, int n, int k0, int slot) {
-  static_assert(64 % NB == 0 && NB <= 32 && R % 32 == 0, "layout: row j < NB must sit in chunk 0");
-  constexpr int CPW = 64 / NB;
-  constexpr int NCH = NW * CPW;
-  constexpr int XS = R + 4;  // padded chunk stride in LDS (spreads chunks over banks)
-  constexpr int NSUB = R / 32;
-
-  const int64_t b = blockIdx.x;
-  const int m = n - k0;
-  const int w = m < NB ? m : NB;
-  const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
-  const int c = lane % NB;
-  const int qw = lane / NB;
-  const int q = wave * CPW + qw;
-  const int row0 = q * R;
-  float* colp = H + b * hs0 + (int64_t)(k0 + c) * ldh + k0;
-
-  __shared__ __attribute__((aligned(16))) float xs[NCH * XS];
-  __shared__ float2 red[2][NW][NB];
-  __shared__ float ys[NB][NB + 1];
-  __shared__ float taus[NB];
-
-  // rows held as NSUB sub-vectors of 32 so a uniform index stays in VGPRs
-  v32 av[NSUB];
-#define A_(i) av[(i) >> 5][(i) & 31]
-  const bool colok = c < w;
-#pragma unroll
-  for (int i = 0; i < R; i += 4) {
-    const int r = row0 + i;
-    if constexpr (VEC) {
-      f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (colok && r < m) v = *reinterpret_cast<const f32x4*>(colp + r);
-      A_(i) = v[0];
-      A_(i + 1) = v[1];
-      A_(i + 2) = v[2];
-      A_(i + 3) = v[3];
-    } else {
-#pragma unroll
-      for (int u = 0; u < 4; ++u) A_(i + u) = (colok && r + u < m) ? colp[r + u] : 0.0f;
-    }
-  }
-  float* xq = xs + q * XS;
-  float my_inv = 0.0f;  // 1 / (alpha - beta) of this lane's column, once factored
-
-  for (int j = 0; j < w; ++j) {
-    const int par = j & 1;
-    // j < NB <= 32 <= R: row j is row j of chunk 0, element j of sub-vector 0
-    const int ju = __builtin_amdgcn_readfirstlane(j);
-    if (c == j) {
-#pragma unroll
-      for (int i = 0; i < R; i += 4) {
-        f32x4 v;
-        v[0] = (row0 + i + 0 > j) ? A_(i + 0) : 0.0f;
-        v[1] = (row0 + i + 1 > j) ? A_(i + 1) : 0.0f;
-        v[2] = (row0 + i + 2 > j) ? A_(i + 2) : 0.0f;
-        v[3] = (row0 + i + 3 > j) ? A_(i + 3) : 0.0f;
-        *reinterpret_cast<f32x4*>(xq + i) = v;
-      }
-    }
-    wave_lds_sync();
-    float g0 = 0.0f, g1 = 0.0f, g2 = 0.0f, g3 = 0.0f;
-#pragma unroll
-    for (int i = 0; i < R; i += 4) {
-      const f32x4 x = *reinterpret_cast<const f32x4*>(xq + i);
-      g0 = fmaf(x[0], A_(i + 0), g0);
-      g1 = fmaf(x[1], A_(i + 1), g1);
-      g2 = fmaf(x[2], A_(i + 2), g2);
-      g3 = fmaf(x[3], A_(i + 3), g3);
-    }
-    float g = (g0 + g1) + (g2 + g3);
-    float rowv = (q == 0) ? av[0][ju] : 0.0f;
-    if constexpr (CPW >= 2) {
-      if constexpr (NB == 32) {
-        g = xor32_sum(g);
-        rowv = xor32_sum(rowv);
-      } else {
-        g += xor_lane<NB>(g);
-        rowv += xor_lane<NB>(rowv);
-      }
-    }
-    if constexpr (CPW >= 4) {
-      g += xor_lane<2 * NB>(g);
-      rowv += xor_lane<2 * NB>(rowv);
-    }
-    if constexpr (CPW >= 8) {
-      g += xor_lane<4 * NB>(g);
-      rowv += xor_lane<4 * NB>(rowv);
-    }
-    if (qw == 0) red[par][wave][c] = make_float2(g, rowv);
-    __syncthreads();
-    float tot = 0.0f, rowt = 0.0f;
-#pragma unroll
-    for (int wv = 0; wv < NW; ++wv) {
-      const float2 t = red[par][wv][c];
-      tot += t.x;
-      rowt += t.y;
-    }
-    const float sigma = readlane(tot, j);
-    const float alpha = readlane(rowt, j);
-    const Reflector rf = make_reflector(alpha, sigma);
-    // Finished columns c < j keep their unscaled x_c (v_c = x_c * inv_c is
-    // applied after the loop), so here z_c = inv_c * (v_c^T v).
-    const float z = fmaf(tot, rf.inv, rowt);
-    const float s = (c > j && c < w) ? rf.tau * z : 0.0f;
-    if (wave == 0 && qw == 0) {
-      ys[c][j] = (c < j) ? my_inv * z : z;
-      if (c == j) taus[j] = rf.tau;
-    }
-    if (c == j) my_inv = rf.inv;
-    // a_r[c] -= tau z_c v_r with v_r = x_r * inv  (s == 0 on columns c <= j)
-    const float alp = -s * rf.inv;
-#pragma unroll
-    for (int i = 0; i < R; i += 4) {
-      const f32x4 x = *reinterpret_cast<const f32x4*>(xq + i);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) A_(i + u) = fmaf(x[u], alp, A_(i + u));
-    }
-    if (q == 0) {
-      const float aj = av[0][ju];
-      av[0][ju] = (c == j) ? rf.beta : aj - s;
-    }
-    // the next step's publish reuses xq: keep this step's reads ahead of it
-    wave_lds_sync();
-  }
-
-  // v_c = x_c * inv_c below the diagonal (opaque row base: the masks are not
-  // hoisted above the loop, where they would stay live in registers)
-  {
-    int r0v = row0, cv = c;
-    asm volatile("" : "+v"(r0v), "+v"(cv));
-#pragma unroll
-    for (int i = 0; i < R; ++i)
-      if (r0v + i > cv) A_(i) *= my_inv;
-  }
-
-#pragma unroll
-  for (int i = 0; i < R; i += 4) {
-    const int r = row0 + i;
-    if constexpr (VEC) {
-      if (colok && r < m) {
-        f32x4 v = {A_(i), A_(i + 1), A_(i + 2), A_(i + 3)};
-        *reinterpret_cast<f32x4*>(colp + r) = v;
-      }
-    } else {
-#pragma unroll
-      for (int u = 0; u < 4; ++u)
-        if (colok && r + u < m) colp[r + u] = A_(i + u);
-    }
-  }
-
-#undef A_
-  // T factor (slarft recurrence) from the stored y_p^(j) = v_p^T v_j:
-  //   T[i][j] = -tau_j * sum_{i <= p < j} T[i][p] y_p^(j),  T[j][j] = tau_j
-  __syncthreads();
-  if (wave == 0 && lane < NB) {
-    float trow[NB];
-#pragma unroll
-    for (int jj = 0; jj < NB; ++jj) {
-      float acc = 0.0f;
-#pragma unroll
-      for (int p = 0; p < jj; ++p) acc = fmaf(trow[p], ys[p][jj], acc);
-      const float tj = (jj < w) ? taus[jj] : 0.0f;
-      trow[jj] = (lane < jj) ? -tj * acc : (lane == jj ? tj : 0.0f);
-    }
-    float* Tb = Tws + ((b * kMaxSlots + slot) * 32 + lane) * 32;
-#pragma unroll
-    for (int jj = 0; jj < NB; ++jj) Tb[jj] = trow[jj];
-    if (lane < w) tau[b * ts0 + (int64_t)(k0 + lane) * ts1] = taus[lane];
-  }
-}
-
-// ---------------------------------------------------------------------------
 // Trailing update  A2 <- A2 - V T^T V^T A2  (fp32 MFMA 32x32x2)
 // ---------------------------------------------------------------------------
-// V element (global row, reflector index) of the panel starting at k0.
-__device__ __forceinline__ float v_elem(const float* __restrict__ Hb, int64_t ldh, int n, int k0, int w,
-                                        int row, int refl) {
-  const int rr = row - k0;
-  if (refl >= w || row >= n || rr < refl) return 0.0f;
-  if (rr == refl) return 1.0f;
-  return Hb[(int64_t)(k0 + refl) * ldh + row];
-}
-
-__device__ __forceinline__ float v_fix(float loaded, int rr, int refl, int w) {
-  return (refl >= w || rr < refl) ? 0.0f : (rr == refl ? 1.0f : loaded);
-}
-
-// Load the 32x32 tile of column `col` rows r0.. into the MFMA C layout:
-// reg 4q+i <- row r0 + 8q + 4h + i.
-template <bool VEC>
-__device__ __forceinline__ void load_ctile(const float* __restrict__ Hb, int64_t ldh, int n, int r0, int col,
-                                           bool colok, int h, float (&x)[16]) {
-  const float* cp = Hb + (int64_t)col * ldh;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int rb = r0 + 8 * q + 4 * h;
-    if constexpr (VEC) {
-      f32x4 v = {0.0f, 0.0f, 0.0f, 0.0f};
-      if (colok && rb < n) v = *reinterpret_cast<const f32x4*>(cp + rb);
-      x[4 * q + 0] = v[0];
-      x[4 * q + 1] = v[1];
-      x[4 * q + 2] = v[2];
-      x[4 * q + 3] = v[3];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) x[4 * q + i] = (colok && rb + i < n) ? cp[rb + i] : 0.0f;
-    }
-  }
-}
-
-template <bool VEC>
-__device__ __forceinline__ void store_ctile(float* __restrict__ Hb, int64_t ldh, int n, int r0, int col,
-                                            bool colok, int h, const f32x16& x) {
-  if (!colok) return;
-  float* cp = Hb + (int64_t)col * ldh;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int rb = r0 + 8 * q + 4 * h;
-    if constexpr (VEC) {
-      if (rb < n) {
-        f32x4 v = {x[4 * q + 0], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]};
-        *reinterpret_cast<f32x4*>(cp + rb) = v;
-      }
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i)
-        if (rb + i < n) cp[rb + i] = x[4 * q + i];
-    }
-  }
-}
-
 // Applies `nwy` consecutive compact-WY transforms, panel i starting at row and
 // column kw = k0 + i*nb with width nb (<= 32) and T factor Tws slot
 // (slot0 + i), to the 32-column strip  [c_begin + 32*blockIdx.x, +32) of
@@ -564,62 +294,6 @@ hipError_t launch_copy_colmajor(const float* A, int64_t batch, int n, int64_t as
   const int ntile = (n + 63) / 64;
   hipLaunchKernelGGL(copy_to_colmajor_kernel, dim3(ntile * ntile, (unsigned)batch), dim3(256), 0, stream, A,
                      as0, as1, as2, H, hs0, ldh, n, ntile);
-  return hipGetLastError();
-}
-
-int panel_width_for(int m) { return m > 4096 ? 8 : (m > 2048 ? 16 : 32); }
-
-hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float* tau, int64_t ts0,
-                        int64_t ts1, float* Tws, int n, int k0, int nb, int m_cap, int slot, bool vec,
-                        hipStream_t stream) {
-  // template chosen for m_cap rows (the tallest panel of its group) and width nb;
-  // rows covered = NW * (64 / NB) * R
-  const int m = m_cap;
-  const dim3 grid((unsigned)batch);
-#define FASTQR_PANEL(NB, NW, R)                                                                           \
-  do {                                                                                                    \
-    if (vec)                                                                                              \
-      hipLaunchKernelGGL((panel_kernel<NB, NW, R, true>), grid, dim3(NW * 64), 0, stream, H, hs0, ldh, tau, \
-                         ts0, ts1, Tws, n, k0, slot);                                                     \
-    else                                                                                                  \
-      hipLaunchKernelGGL((panel_kernel<NB, NW, R, false>), grid, dim3(NW * 64), 0, stream, H, hs0, ldh,    \
-                         tau, ts0, ts1, Tws, n, k0, slot);                                                \
-  } while (0)
-  if (nb == 32 && m <= 2048) return launch_panel32(H, batch, hs0, ldh, tau, ts0, ts1, Tws, n, k0, slot, stream);
-  if (nb == 32) {
-    if (m <= 128) {
-      FASTQR_PANEL(32, 2, 32);
-    } else if (m <= 256) {
-      FASTQR_PANEL(32, 4, 32);
-    } else if (m <= 512) {
-      FASTQR_PANEL(32, 4, 64);
-    } else if (m <= 1024) {
-      FASTQR_PANEL(32, 8, 64);
-    } else if (m <= 2048) {
-      FASTQR_PANEL(32, 16, 64);
-    } else {
-      return hipErrorInvalidValue;
-    }
-  } else if (nb == 16) {
-    if (m <= 2048) {
-      FASTQR_PANEL(16, 16, 32);
-    } else if (m <= 4096) {
-      FASTQR_PANEL(16, 16, 64);
-    } else {
-      return hipErrorInvalidValue;
-    }
-  } else if (nb == 8) {
-    if (m <= 4096) {
-      FASTQR_PANEL(8, 16, 32);
-    } else if (m <= 8192) {
-      FASTQR_PANEL(8, 16, 64);
-    } else {
-      return hipErrorInvalidValue;
-    }
-  } else {
-    return hipErrorInvalidValue;
-  }
-#undef FASTQR_PANEL
   return hipGetLastError();
 }
 

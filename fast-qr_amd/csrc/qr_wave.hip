@@ -24,13 +24,6 @@ namespace fastqr {
 
 namespace {
 
-// v(lane) + v(lane ^ 16): the two results of one v_permlane16_swap(v, v) are
-// {v_l, v_(l^16)} in some order in every lane.
-__device__ __forceinline__ float xor16_sum(float v) {
-  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(v), __float_as_uint(v), false, false);
-  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
-}
-
 // lane J of this lane's 16-lane row
 template <int J>
 __device__ __forceinline__ float row_bcast(float v) {
@@ -47,19 +40,6 @@ struct make_seq<0, I...> {
 };
 
 }  // namespace
-
-// Reflector without branches (sigma is wave-uniform; selects keep the step
-// free of scalar branches).  Same values as make_reflector.
-__device__ __forceinline__ Reflector make_reflector_sel(float alpha, float sigma) {
-  const float nrm = __builtin_amdgcn_sqrtf(fmaf(alpha, alpha, sigma));
-  const float bt = (alpha >= 0.0f) ? -nrm : nrm;
-  const bool act = sigma > 0.0f;
-  Reflector r;
-  r.tau = act ? (bt - alpha) * __builtin_amdgcn_rcpf(bt) : 0.0f;
-  r.inv = act ? __builtin_amdgcn_rcpf(alpha - bt) : 0.0f;
-  r.beta = act ? bt : alpha;
-  return r;
-}
 
 template <int NT>
 struct WaveQR {
