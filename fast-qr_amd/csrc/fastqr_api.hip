@@ -35,6 +35,12 @@ int hip_fail(hipError_t e, const char* what) {
 
 constexpr int64_t kMaxN = 4096;
 constexpr int kWaveMaxN = 64;
+// Tall matrices use the row-split trailing update (a 32-column strip of more
+// than 2048 rows does not fit in one workgroup's registers, and small batches
+// leave most of the GPU idle with one workgroup per strip).
+constexpr int64_t kRowSplitMinN = 2049;
+
+bool use_rowsplit(int64_t /*batch*/, int64_t n) { return n >= kRowSplitMinN; }
 
 bool ranges_overlap(const float* a, int64_t a_elems, const float* b, int64_t b_elems) {
   const uintptr_t a0 = (uintptr_t)a, a1 = a0 + (uintptr_t)a_elems * 4;
@@ -143,6 +149,114 @@ hipError_t timed(int kind, double flops, double bytes, hipStream_t stream, F&& f
   return e;
 }
 
+
+// Blocked QR with the row-split trailing update (tall matrices).  Panels are
+// grouped (up to kMaxWY panels, at most kWyrMaxK columns).  On the side stream:
+// each panel, then a row-split update of the rest of its group by that panel;
+// after the group its T factors and Gram matrix are joined into the group T and
+// the group is applied to the next group's columns (look-ahead).  On the
+// caller's stream the group is applied to everything right of the next group,
+// overlapping the next group's panels.  Two scratch areas (one per stream) and
+// two banks of T slots and group T alternate by group parity.
+int run_rowsplit(float* H, int64_t batch, int64_t hs0, int64_t ldh, float* tau, int64_t ts0, int64_t ts1, float* Tws,
+                 int n, bool vec, hipStream_t stream) {
+  using fastqr::WyrCall;
+  const int64_t slot_floats = batch * fastqr::kMaxSlots * 1024;
+  float* Tg0 = Tws + slot_floats;
+  float* area[2] = {Tg0 + 2 * batch * fastqr::kWyrTgStride, nullptr};
+  area[1] = area[0] + fastqr::wyr_workspace_floats(batch, n);
+  const double bd = (double)batch;
+
+  struct Group {
+    int g0, nb, g_end, npan, slot_base;
+  };
+  std::vector<Group> groups;
+  for (int g0 = 0, gi = 0; g0 < n; ++gi) {
+    const int nb = fastqr::panel_width_for(n - g0);
+    const int span = fastqr::kMaxWY * nb < fastqr::kWyrMaxK ? fastqr::kMaxWY * nb : fastqr::kWyrMaxK;
+    const int g_end = (g0 + span < n) ? g0 + span : n;
+    groups.push_back(Group{g0, nb, g_end, (g_end - g0 + nb - 1) / nb, (gi & 1) * fastqr::kMaxWY});
+    g0 = g_end;
+  }
+  DeviceAux* aux = device_aux();
+  if (!aux) return fail(FASTQR_EINVAL, "cannot create the side stream");
+  const hipStream_t side = aux->side;
+  auto join = [&](hipStream_t waiter, hipStream_t signaller) -> hipError_t {
+    hipEvent_t ev = aux->take();
+    if (!ev) return hipErrorOutOfMemory;
+    hipError_t e = hipEventRecord(ev, signaller);
+    if (e == hipSuccess) e = hipStreamWaitEvent(waiter, ev, 0);
+    return e;
+  };
+  auto base_call = [&](int kv, int k, int c_begin, int c_end, float* scratch) {
+    WyrCall c{};
+    c.H = H;
+    c.hs0 = hs0;
+    c.ldh = (int)ldh;
+    c.n = n;
+    c.batch = batch;
+    c.kv = kv;
+    c.k = k;
+    c.c_begin = c_begin;
+    c.c_end = c_end;
+    c.Tws = Tws;
+    c.scratch = scratch;
+    c.rows_per_blk = fastqr::wyr_rows_per_block(n - kv, batch, c_end - c_begin);
+    c.vec = vec;
+    return c;
+  };
+  auto run_wyr = [&](const WyrCall& c, hipStream_t st) -> hipError_t {
+    const double m = n - c.kv, k = c.k;
+    const double cx = c.c_end - c.c_begin - (c.gram ? 32.0 * ((c.k + 31) / 32) : 0.0);
+    return timed(kUpdate, bd * 4.0 * m * k * cx, bd * (12.0 * m * cx + 8.0 * m * k), st,
+                 [&] { return fastqr::launch_wyr(c, st); });
+  };
+
+  hipError_t e = join(side, stream);  // the side stream starts after the copy
+  if (e != hipSuccess) return hip_fail(e, "stream join");
+  std::vector<bool> rest_done(groups.size(), false);
+  for (size_t gi = 0; gi < groups.size(); ++gi) {
+    const Group& G = groups[gi];
+    for (int i = 0; i < G.npan; ++i) {
+      const int pk = G.g0 + i * G.nb;
+      const double m = n - pk;
+      const int w = (n - pk < G.nb) ? n - pk : G.nb;
+      e = timed(kPanel, bd * (2.0 * m * w * w - 2.0 * w * w * w / 3.0), bd * 8.0 * m * w, side, [&] {
+        return fastqr::launch_panel(H, batch, hs0, ldh, tau, ts0, ts1, Tws, n, pk, G.nb, n - pk, G.slot_base + i, vec,
+                                    side);
+      });
+      if (e != hipSuccess) return hip_fail(e, "panel launch");
+      if (pk + w < G.g_end) {
+        WyrCall c = base_call(pk, w, pk + w, G.g_end, area[0]);
+        c.Tslot = Tws + (G.slot_base + i) * 1024;
+        if ((e = run_wyr(c, side)) != hipSuccess) return hip_fail(e, "narrow update launch");
+      }
+    }
+    if (gi + 1 == groups.size()) break;
+    const Group& Nx = groups[gi + 1];
+    float* Tg = Tg0 + (int64_t)(gi & 1) * batch * fastqr::kWyrTgStride;
+    // the next group's columns last received the previous group's wide update
+    if (gi >= 1 && rest_done[gi - 1] && (e = join(side, stream)) != hipSuccess) return hip_fail(e, "stream join");
+    WyrCall c = base_call(G.g0, G.g_end - G.g0, G.g0, Nx.g_end, area[0]);
+    c.gram = true;
+    c.use_tg = true;
+    c.q = G.npan;
+    c.nb = G.nb;
+    c.slot0 = G.slot_base;
+    c.Tg = Tg;
+    if ((e = run_wyr(c, side)) != hipSuccess) return hip_fail(e, "look-ahead update launch");
+    if (Nx.g_end < n) {
+      if ((e = join(stream, side)) != hipSuccess) return hip_fail(e, "stream join");
+      WyrCall r = base_call(G.g0, G.g_end - G.g0, Nx.g_end, n, area[1]);
+      r.use_tg = true;
+      r.Tg = Tg;
+      if ((e = run_wyr(r, stream)) != hipSuccess) return hip_fail(e, "trailing update launch");
+      rest_done[gi] = true;
+    }
+  }
+  if ((e = join(stream, side)) != hipSuccess) return hip_fail(e, "stream join");
+  return FASTQR_OK;
+}
 }  // namespace
 
 extern "C" {
@@ -183,9 +297,11 @@ const char* fastqr_path_name(int64_t n) {
 }
 
 size_t fastqr_workspace_bytes(int64_t batch, int64_t n) {
-  if (batch <= 0 || n <= kWaveMaxN) return 0;
-  const size_t t_bytes = (size_t)batch * fastqr::kMaxSlots * 32 * 32 * sizeof(float);
-  return (t_bytes + 255) & ~(size_t)255;
+  if (batch <= 0 || n <= kWaveMaxN || n > kMaxN) return 0;
+  size_t floats = (size_t)batch * fastqr::kMaxSlots * 32 * 32;
+  if (use_rowsplit(batch, n))
+    floats += 2 * (size_t)batch * fastqr::kWyrTgStride + 2 * fastqr::wyr_workspace_floats(batch, (int)n);
+  return (floats * sizeof(float) + 255) & ~(size_t)255;
 }
 
 int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a_s1, int64_t a_s2,
@@ -256,6 +372,8 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
     });
     if (e != hipSuccess) return hip_fail(e, "copy launch");
   }
+  if (use_rowsplit(batch, n)) return run_rowsplit(H, batch, h_s0, h_s2, tau, tau_s0, tau_s1, Tws, ni, vec, stream);
+
   // Panels are processed in groups of up to kMaxWY.  Within a group each
   // panel is followed by a narrow update of the group's remaining columns;
   // the group's transforms are then applied together to the columns right of

@@ -32,6 +32,35 @@ hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, c
                             int k0, int nb, int slot0, int nwy, int c_begin, int c_end, bool vec,
                             hipStream_t stream);
 
+// Row-split compact-WY update (qr_update.hip): for tall matrices and small
+// batches the trailing update is split over row blocks as well as column
+// strips (partial V^T X per row block, W = -T^T P, X += V W).
+constexpr int kWyrMaxBlk = 4;                  // reflector blocks of 32 per update
+constexpr int kWyrMaxK = 32 * kWyrMaxBlk;      // reflectors per update (a group of panels)
+constexpr int kWyrTgLd = kWyrMaxK;             // leading dimension of a group T
+constexpr int64_t kWyrTgStride = (int64_t)kWyrMaxK * kWyrMaxK;  // floats per matrix per group-T bank
+
+struct WyrCall {
+  float* H;
+  int64_t hs0;
+  int ldh, n;
+  int64_t batch;
+  int kv, k;            // reflectors: columns [kv, kv + k) of H, rows [kv, n)
+  int c_begin, c_end;   // columns to read; with gram the first ceil(k/32) strips are the group's own
+  bool gram;            // form the group T (Gram V^T V + panel T join) into Tg
+  bool use_tg;          // take T from Tg (k x k) instead of the single panel slot Tslot
+  int q, nb, slot0;     // the group's panels (count, width, first T slot) for the join
+  const float* Tws;     // T slots (kMaxSlots per matrix)
+  const float* Tslot;   // T of a single panel: slot base, per-matrix stride kMaxSlots * 1024
+  float* Tg;            // group T bank, per-matrix stride kWyrTgStride
+  float* scratch;       // partial products and W (wyr_workspace_floats(batch, n) floats)
+  int rows_per_blk;     // multiple of 32
+  bool vec;
+};
+hipError_t launch_wyr(const WyrCall& c, hipStream_t stream);
+int wyr_rows_per_block(int m, int64_t batch, int cols);
+size_t wyr_workspace_floats(int64_t batch, int n);
+
 // Panels per group: the wide trailing update applies this many transforms at once.
 constexpr int kMaxWY = 4;
 // T-factor slots per matrix in the workspace (32 x 32 floats each): two

@@ -13,6 +13,7 @@
 //                     the row sum is valid), so no register shuffles are needed.
 #include "device.hpp"
 #include "kernels.hpp"
+#include "wy.hpp"
 
 namespace fastqr {
 
@@ -55,109 +56,6 @@ __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __re
 // ---------------------------------------------------------------------------
 // Trailing update  A2 <- A2 - V T^T V^T A2  (fp32 MFMA 32x32x2)
 // ---------------------------------------------------------------------------
-// Applies `nwy` consecutive compact-WY transforms, panel i starting at row and
-// column kw = k0 + i*nb with width nb (<= 32) and T factor Tws slot
-// (slot0 + i), to the 32-column strip  [c_begin + 32*blockIdx.x, +32) of
-// columns in [c_begin, c_end), rows [k0, n).  The strip is split into 32-row
-// tiles; wave w owns tiles w, w+NW, ...  With RES the tiles stay in the MFMA
-// accumulator layout in VGPRs for all transforms (one load, one store per
-// element); otherwise (taller strips) every transform streams them twice.
-// Per transform:  P = V^T X  (16 MFMAs per tile, the X registers used as the
-// B operand through the contraction-index permutation), P summed over waves
-// in LDS, W = -(T^T P) (16 MFMAs), X += V W (16 MFMAs per tile).
-// Column-major matrix accessed through a buffer descriptor: element (row, col)
-// at byte offset 4 * (col * ldh + row).  n <= 8192 and ldh * n < 2^29 keep the
-// offsets within 32 bits (checked by the host).
-struct MatBuf {
-  rsrc_t r;
-  int ldh;
-  int n;
-  __device__ __forceinline__ uint32_t off(int row, int col) const { return 4u * (uint32_t)(col * ldh + row); }
-};
-
-// 32-row tile of column `col` (rows r0.., MFMA accumulator layout: register
-// 4q+i <- row r0 + 8q + 4h + i); rows >= n and !ok read as 0.
-template <bool VEC>
-__device__ __forceinline__ f32x16 tile_load(const MatBuf& M, int r0, int col, bool ok, int h) {
-  f32x16 x;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int rb = r0 + 8 * q + 4 * h;
-    if constexpr (VEC) {
-      const f32x4 v = buf_load4(M.r, (ok && rb < M.n) ? M.off(rb, col) : kOffNone);
-#pragma unroll
-      for (int i = 0; i < 4; ++i) x[4 * q + i] = v[i];
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) x[4 * q + i] = buf_load(M.r, (ok && rb + i < M.n) ? M.off(rb + i, col) : kOffNone);
-    }
-  }
-  return x;
-}
-
-template <bool VEC>
-__device__ __forceinline__ void tile_store(const MatBuf& M, int r0, int col, bool ok, int h, const f32x16& x) {
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int rb = r0 + 8 * q + 4 * h;
-    if constexpr (VEC) {
-      f32x4 v = {x[4 * q + 0], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]};
-      buf_store4(M.r, (ok && rb < M.n) ? M.off(rb, col) : kOffNone, v);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) buf_store(M.r, (ok && rb + i < M.n) ? M.off(rb + i, col) : kOffNone, x[4 * q + i]);
-    }
-  }
-}
-
-// P += V^T X for one 32-row tile at r0 of the transform whose reflectors start
-// at row/column kw (width nb).  V pattern A: lane holds rows r0 + 8q + 4h + i
-// of reflector l32, loaded 4 rows at a time.
-template <bool VEC>
-__device__ __forceinline__ void wy_accumulate(f32x16& P, const f32x16& X, const MatBuf& M, int kw, int nb, int r0,
-                                              int h, int l32) {
-  const int refl = l32;
-  const bool active = refl < nb;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int rb = r0 + 8 * q + 4 * h;
-    f32x4 v;
-    if constexpr (VEC) {
-      v = buf_load4(M.r, (active && rb < M.n) ? M.off(rb, kw + refl) : kOffNone);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = buf_load(M.r, (active && rb + i < M.n) ? M.off(rb + i, kw + refl) : kOffNone);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rr = rb + i - kw;  // row within the transform's panel
-      const float vv = (rr < refl) ? 0.0f : (rr == refl ? 1.0f : v[i]);
-      P = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, X[4 * q + i], P, 0, 0, 0);
-    }
-  }
-}
-
-// X += V W for one tile.  V pattern B: lane holds row r0 + l32 of reflector
-// 8q + 4h + i.
-__device__ __forceinline__ void wy_apply(f32x16& X, const f32x16& W, const MatBuf& M, int kw, int nb, int r0, int h,
-                                         int l32) {
-  const int row = r0 + l32;
-  const int rr = row - kw;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    float vb[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int refl = 8 * q + 4 * h + i;
-      const bool load = refl < nb && rr > refl && row < M.n;
-      const float v = buf_load(M.r, load ? M.off(row, kw + refl) : kOffNone);
-      vb[i] = (refl < nb && rr == refl) ? 1.0f : v;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) X = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[i], W[4 * q + i], X, 0, 0, 0);
-  }
-}
-
 // Applies `nwy` consecutive compact-WY transforms, transform i starting at
 // row and column kw = k0 + i*nb with width nb (<= 32) and T factor in
 // workspace slot (slot0 + i), to the 32-column strip

@@ -413,6 +413,7 @@ hipError_t launch_panel_cfg(int nw, int tpw, float* H, int64_t batch, int64_t hs
   FASTQR_PANEL(8, 16, 2)
   FASTQR_PANEL(8, 16, 1)
   FASTQR_PANEL(8, 32, 1)
+  FASTQR_PANEL(8, 8, 2)
 #undef FASTQR_PANEL
   return hipErrorInvalidValue;
 }

@@ -1,0 +1,363 @@
+// qr_update.hip — row-split compact-WY trailing update for tall matrices and
+// small batches.
+//
+// Reference counterpart: blocked{n}_trailing_update_kernel,
+// submissions/candidate.py:2507-2716 (compact-WY mode, 2586-2672), which gives
+// each CTA whole columns of the trailing matrix; with a batch of 2 or 8 that
+// leaves most of the GPU idle, and a 4096-row strip does not fit in one
+// workgroup's registers.  Here the rows are split too:
+//
+//   X <- X - V (T^T (V^T X))      V: m x k (k <= 128 reflectors of up to four
+//                                 consecutive panels), T: k x k, X: m x c
+//
+//   wyr_partial_kernel  grid (32-column strips, row blocks, batch), one wave:
+//                       P_rb = V_rb^T X_rb for its row block (fp32 MFMA
+//                       32x32x2, X tiles as the B operand in accumulator
+//                       layout).  Strips inside the group's own columns are
+//                       read as V (unit diagonal, zeros above), which gives the
+//                       Gram matrix V^T V the group T needs.
+//   wyr_tg_kernel       one workgroup per matrix: sums the Gram partials and
+//                       joins the panels' T factors into the group T
+//                       (T_[1:j] = [[T_[1:j-1], -T_[1:j-1] G_[1:j-1,j] T_j], [0, T_j]]).
+//   wyr_w_kernel        one wave per strip: W = -T^T sum_rb P_rb.
+//   wyr_apply_kernel    grid (strips, row blocks, batch), one wave: X_rb += V_rb W.
+//
+// Partial products are summed in a fixed order (no atomics), so results are
+// bitwise reproducible.
+#include "device.hpp"
+#include "kernels.hpp"
+#include "wy.hpp"
+
+namespace fastqr {
+
+namespace {
+
+// Partial-product layout: one 32x32 block = 16 accumulator registers x 64
+// lanes, register-major, so each lane reads and writes 16 strided floats and
+// every access instruction is one coalesced 256-byte row.
+__device__ __forceinline__ void store_acc(float* __restrict__ dst, const f32x16& v, int lane) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) dst[j * 64 + lane] = v[j];
+}
+
+__device__ __forceinline__ f32x16 load_acc(const float* __restrict__ src, int lane) {
+  f32x16 v;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) v[j] = src[j * 64 + lane];
+  return v;
+}
+
+// row within a 32x32 block held by register j of a lane in half h
+__device__ __forceinline__ int acc_row(int j, int h) { return 8 * (j >> 2) + 4 * h + (j & 3); }
+
+}  // namespace
+
+// Ppart index of (matrix b, strip s, row block rb, reflector block blk)
+__device__ __forceinline__ int64_t pp_index(int64_t b, int s, int rb, int blk, int nstrips, int nrb) {
+  return (((b * nstrips + s) * nrb + rb) * kWyrMaxBlk + blk) * 1024;
+}
+
+template <int NBLK, bool VEC>
+__global__ void __launch_bounds__(64) wyr_partial_kernel(const float* __restrict__ H, int64_t hs0, int ldh, int n,
+                                                         int kv, int k, int c_begin, int c_end, int gram_end,
+                                                         int rows_per_blk, float* __restrict__ Ppart, int nstrips,
+                                                         int nrb) {
+  const int s = blockIdx.x, rb = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int lane = threadIdx.x, h = lane >> 5, l32 = lane & 31;
+  const int col = c_begin + 32 * s + l32;
+  const bool colok = col < c_end;
+  const bool is_v = col < gram_end;
+  const MatBuf M{make_rsrc(H + b * hs0, (uint32_t)(4 * ldh * n)), ldh, n};
+  const int r_lo = kv + rb * rows_per_blk;
+  const int r_hi = min(n, r_lo + rows_per_blk);
+
+  f32x16 P[NBLK];
+#pragma unroll
+  for (int blk = 0; blk < NBLK; ++blk)
+#pragma unroll
+    for (int j = 0; j < 16; ++j) P[blk][j] = 0.0f;
+
+  for (int r0 = r_lo; r0 < r_hi; r0 += 32) {
+    f32x16 X = tile_load<VEC>(M, r0, col, colok, h);
+    if (is_v) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int row = r0 + acc_row(j, h);
+        X[j] = row < col ? 0.0f : (row == col ? 1.0f : X[j]);
+      }
+    }
+#pragma unroll
+    for (int blk = 0; blk < NBLK; ++blk) {
+      const int kw = kv + 32 * blk;
+      const int nbv = min(32, k - 32 * blk);
+      if (r0 + 32 > kw) wy_accumulate<VEC>(P[blk], X, M, kw, nbv, r0, h, l32);
+    }
+  }
+#pragma unroll
+  for (int blk = 0; blk < NBLK; ++blk) store_acc(Ppart + pp_index(b, s, rb, blk, nstrips, nrb), P[blk], lane);
+}
+
+// Sum the row-block partials of strips [0, gridDim.x) into Gsum (the Gram
+// matrix V^T V of the group's own strips): one wave per (strip, block, matrix).
+__global__ void __launch_bounds__(64) wyr_reduce_kernel(const float* __restrict__ Ppart, int nstrips, int nrb,
+                                                        float* __restrict__ Gsum) {
+  const int s = blockIdx.x, blk = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int lane = threadIdx.x;
+  f32x16 acc;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+  int rb = 0;
+  for (; rb + 4 <= nrb; rb += 4) {
+    f32x16 v[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) v[u] = load_acc(Ppart + pp_index(b, s, rb + u, blk, nstrips, nrb), lane);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) acc += v[u];
+  }
+  for (; rb < nrb; ++rb) acc += load_acc(Ppart + pp_index(b, s, rb, blk, nstrips, nrb), lane);
+  store_acc(Gsum + ((b * kWyrMaxBlk + blk) * kWyrMaxBlk + s) * 1024, acc, lane);
+}
+
+// Group T (k x k, leading dimension kWyrTgLd) from the Gram matrix (Gsum) and
+// the panels' T factors (q panels of width nb in workspace slots slot0 ..).
+__global__ void __launch_bounds__(1024) wyr_tg_kernel(const float* __restrict__ Gsum, const float* __restrict__ Tws,
+                                                      int slot0, int q, int nb, int k, float* __restrict__ Tg) {
+  const int64_t b = blockIdx.x;
+  const int tid = threadIdx.x;
+  __shared__ float Gs[kWyrMaxK][kWyrMaxK + 1];
+  __shared__ float Ts[kWyrMaxK][kWyrMaxK + 1];
+  __shared__ float Mt[kWyrMaxK][33];
+  const int nblk = (k + 31) / 32;
+  // block (blk, s) of G = V_blk^T V_s, accumulator layout
+  for (int idx = tid; idx < nblk * nblk * 1024; idx += 1024) {
+    const int lane = idx & 63, j = (idx >> 6) & 15, pair = idx >> 10;
+    const int blk = pair % nblk, s = pair / nblk;
+    Gs[32 * blk + acc_row(j, lane >> 5)][32 * s + (lane & 31)] =
+        Gsum[((b * kWyrMaxBlk + blk) * kWyrMaxBlk + s) * 1024 + j * 64 + lane];
+  }
+  for (int idx = tid; idx < kWyrMaxK * kWyrMaxK; idx += 1024) Ts[idx / kWyrMaxK][idx % kWyrMaxK] = 0.0f;
+  __syncthreads();
+  for (int i = 0; i < q; ++i) {
+    const float* Tp = Tws + (b * kMaxSlots + slot0 + i) * 1024;
+    for (int idx = tid; idx < nb * nb; idx += 1024) {
+      const int r = idx / nb, c = idx % nb;
+      if (i * nb + r < k && i * nb + c < k) Ts[i * nb + r][i * nb + c] = Tp[r * 32 + c];
+    }
+  }
+  __syncthreads();
+  for (int j = 1; j < q; ++j) {
+    const int c0 = j * nb;
+    if (c0 >= k) break;
+    // Mt = G[0:c0, c0:c0+nb] T_j
+    for (int idx = tid; idx < c0 * nb; idx += 1024) {
+      const int r = idx / nb, c = idx % nb;
+      float acc = 0.0f;
+      for (int p = 0; p <= c; ++p) acc = fmaf(Gs[r][c0 + p], Ts[c0 + p][c0 + c], acc);
+      Mt[r][c] = acc;
+    }
+    __syncthreads();
+    // T[0:c0, c0:c0+nb] = -T[0:c0, 0:c0] Mt   (T upper triangular)
+    for (int idx = tid; idx < c0 * nb; idx += 1024) {
+      const int r = idx / nb, c = idx % nb;
+      float acc = 0.0f;
+      for (int p = r; p < c0; ++p) acc = fmaf(Ts[r][p], Mt[p][c], acc);
+      Ts[r][c0 + c] = -acc;
+    }
+    __syncthreads();
+  }
+  float* Tb = Tg + b * kWyrTgStride;
+  for (int idx = tid; idx < kWyrMaxK * kWyrMaxK; idx += 1024) {
+    const int r = idx / kWyrMaxK, c = idx % kWyrMaxK;
+    Tb[r * kWyrTgLd + c] = (r < k && c < k) ? Ts[r][c] : 0.0f;
+  }
+}
+
+// W = -T^T sum_rb P_rb for the strips [s0, s0 + gridDim.x) of Ppart; T is the
+// k x k matrix at Tsrc (+ b * t_stride, leading dimension ldt).
+template <int NBLK>
+__global__ void __launch_bounds__(64) wyr_w_kernel(const float* __restrict__ Ppart, int nstrips, int nrb, int s0,
+                                                   const float* __restrict__ Tsrc, int64_t t_stride, int ldt, int k,
+                                                   float* __restrict__ Wbuf, int nstrips_w) {
+  const int s = blockIdx.x;
+  const int64_t b = blockIdx.y;
+  const int lane = threadIdx.x, h = lane >> 5, l32 = lane & 31;
+  f32x16 P[NBLK];
+#pragma unroll
+  for (int blk = 0; blk < NBLK; ++blk) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) P[blk][j] = 0.0f;
+    int rb = 0;
+    for (; rb + 4 <= nrb; rb += 4) {
+      f32x16 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = load_acc(Ppart + pp_index(b, s0 + s, rb + u, blk, nstrips, nrb), lane);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) P[blk] += v[u];
+    }
+    for (; rb < nrb; ++rb) P[blk] += load_acc(Ppart + pp_index(b, s0 + s, rb, blk, nstrips, nrb), lane);
+  }
+  const float* Tb = Tsrc + b * t_stride;
+#pragma unroll
+  for (int blk = 0; blk < NBLK; ++blk) {
+    f32x16 W;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) W[j] = 0.0f;
+    // W_blk = sum_{blk' <= blk} T(blk', blk)^T P_blk'
+#pragma unroll
+    for (int bp = 0; bp <= blk; ++bp) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int kk = 32 * bp + acc_row(j, h);
+        const int cc = 32 * blk + l32;
+        const float t = (kk < k && cc < k) ? Tb[kk * ldt + cc] : 0.0f;
+        W = __builtin_amdgcn_mfma_f32_32x32x2f32(t, P[bp][j], W, 0, 0, 0);
+      }
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) W[j] = -W[j];
+    store_acc(Wbuf + ((b * nstrips_w + s) * kWyrMaxBlk + blk) * 1024, W, lane);
+  }
+}
+
+template <int NBLK, bool VEC>
+__global__ void __launch_bounds__(64) wyr_apply_kernel(float* __restrict__ H, int64_t hs0, int ldh, int n, int kv,
+                                                       int k, int c_begin, int c_end, int rows_per_blk,
+                                                       const float* __restrict__ Wbuf, int nstrips_w) {
+  const int s = blockIdx.x, rb = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int lane = threadIdx.x, h = lane >> 5, l32 = lane & 31;
+  const int col = c_begin + 32 * s + l32;
+  const bool colok = col < c_end;
+  const MatBuf M{make_rsrc(H + b * hs0, (uint32_t)(4 * ldh * n)), ldh, n};
+  const int r_lo = kv + rb * rows_per_blk;
+  const int r_hi = min(n, r_lo + rows_per_blk);
+  f32x16 W[NBLK];
+#pragma unroll
+  for (int blk = 0; blk < NBLK; ++blk) W[blk] = load_acc(Wbuf + ((b * nstrips_w + s) * kWyrMaxBlk + blk) * 1024, lane);
+  for (int r0 = r_lo; r0 < r_hi; r0 += 32) {
+    f32x16 X = tile_load<VEC>(M, r0, col, colok, h);
+#pragma unroll
+    for (int blk = 0; blk < NBLK; ++blk) {
+      const int kw = kv + 32 * blk;
+      const int nbv = min(32, k - 32 * blk);
+      if (r0 + 32 > kw) wy_apply(X, W[blk], M, kw, nbv, r0, h, l32);
+    }
+    tile_store<VEC>(M, r0, col, colok, h, X);
+  }
+}
+
+// ---------------------------------------------------------------------------
+// Host side
+// ---------------------------------------------------------------------------
+int wyr_rows_per_block(int m, int64_t batch, int cols) {
+  // enough waves to fill the GPU (about 1024 (strip, row block) pairs per
+  // launch) with as few row blocks as possible (each adds a partial to sum)
+  const int64_t strips = (cols + 31) / 32;
+  int r = 512;
+  while (r > 128 && batch * strips * ((m + r - 1) / r) < 1024) r >>= 1;
+  return r;
+}
+
+size_t wyr_workspace_floats(int64_t batch, int n) {
+  const int64_t nstrips = (n + 31) / 32 + kWyrMaxBlk;
+  const int64_t nrb = (n + 127) / 128;
+  const int64_t pp = batch * nstrips * nrb * kWyrMaxBlk * 1024;
+  const int64_t w = batch * nstrips * kWyrMaxBlk * 1024;
+  const int64_t g = batch * kWyrMaxBlk * kWyrMaxBlk * 1024;
+  return (size_t)(pp + w + g);
+}
+
+hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
+  const int m = c.n - c.kv;
+  if (c.c_end <= c.c_begin || m <= 0 || c.k <= 0 || c.k > kWyrMaxK) return hipSuccess;
+  const int nblk = (c.k + 31) / 32;
+  const int nrb = (m + c.rows_per_blk - 1) / c.rows_per_blk;
+  const int nstrips = (c.c_end - c.c_begin + 31) / 32;
+  const int gram_strips = c.gram ? nblk : 0;  // the first strips of [c_begin, c_end) are the group's own columns
+  const int gram_end = c.gram ? c.kv + c.k : 0;
+  float* Ppart = c.scratch;
+  float* Wbuf = c.scratch + (size_t)c.batch * nstrips * nrb * kWyrMaxBlk * 1024;
+  const dim3 gp((unsigned)nstrips, (unsigned)nrb, (unsigned)c.batch);
+#define WYR_PARTIAL(NB_)                                                                                           \
+  do {                                                                                                             \
+    if (c.vec)                                                                                                     \
+      hipLaunchKernelGGL((wyr_partial_kernel<NB_, true>), gp, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv,   \
+                         c.k, c.c_begin, c.c_end, gram_end, c.rows_per_blk, Ppart, nstrips, nrb);                   \
+    else                                                                                                           \
+      hipLaunchKernelGGL((wyr_partial_kernel<NB_, false>), gp, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv,  \
+                         c.k, c.c_begin, c.c_end, gram_end, c.rows_per_blk, Ppart, nstrips, nrb);                   \
+  } while (0)
+  switch (nblk) {
+    case 1: WYR_PARTIAL(1); break;
+    case 2: WYR_PARTIAL(2); break;
+    case 3: WYR_PARTIAL(3); break;
+    default: WYR_PARTIAL(4); break;
+  }
+#undef WYR_PARTIAL
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+
+  const float* Tsrc = c.Tslot;
+  int64_t t_stride = (int64_t)kMaxSlots * 1024;
+  int ldt = 32;
+  if (c.gram) {
+    // Gram strips: sum the partials, then join the panels' T factors
+    float* Gsum = Wbuf + (size_t)c.batch * nstrips * kWyrMaxBlk * 1024;
+    hipLaunchKernelGGL(wyr_reduce_kernel, dim3((unsigned)gram_strips, (unsigned)nblk, (unsigned)c.batch), dim3(64), 0,
+                       stream, Ppart, nstrips, nrb, Gsum);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+    hipLaunchKernelGGL(wyr_tg_kernel, dim3((unsigned)c.batch), dim3(1024), 0, stream, Gsum, c.Tws, c.slot0, c.q, c.nb,
+                       c.k, c.Tg);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (c.use_tg) {
+    Tsrc = c.Tg;
+    t_stride = kWyrTgStride;
+    ldt = kWyrTgLd;
+  }
+  const int nx = nstrips - gram_strips;  // strips that are updated
+  if (nx <= 0) return hipSuccess;
+  const dim3 gw((unsigned)nx, (unsigned)c.batch);
+  switch (nblk) {
+    case 1:
+      hipLaunchKernelGGL((wyr_w_kernel<1>), gw, dim3(64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
+                         ldt, c.k, Wbuf, nx);
+      break;
+    case 2:
+      hipLaunchKernelGGL((wyr_w_kernel<2>), gw, dim3(64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
+                         ldt, c.k, Wbuf, nx);
+      break;
+    case 3:
+      hipLaunchKernelGGL((wyr_w_kernel<3>), gw, dim3(64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
+                         ldt, c.k, Wbuf, nx);
+      break;
+    default:
+      hipLaunchKernelGGL((wyr_w_kernel<4>), gw, dim3(64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
+                         ldt, c.k, Wbuf, nx);
+      break;
+  }
+  if ((e = hipGetLastError()) != hipSuccess) return e;
+  const int xc_begin = c.c_begin + 32 * gram_strips;
+  const dim3 ga((unsigned)nx, (unsigned)nrb, (unsigned)c.batch);
+#define WYR_APPLY(NB_)                                                                                             \
+  do {                                                                                                             \
+    if (c.vec)                                                                                                     \
+      hipLaunchKernelGGL((wyr_apply_kernel<NB_, true>), ga, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv, c.k, \
+                         xc_begin, c.c_end, c.rows_per_blk, Wbuf, nx);                                             \
+    else                                                                                                           \
+      hipLaunchKernelGGL((wyr_apply_kernel<NB_, false>), ga, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv,    \
+                         c.k, xc_begin, c.c_end, c.rows_per_blk, Wbuf, nx);                                        \
+  } while (0)
+  switch (nblk) {
+    case 1: WYR_APPLY(1); break;
+    case 2: WYR_APPLY(2); break;
+    case 3: WYR_APPLY(3); break;
+    default: WYR_APPLY(4); break;
+  }
+#undef WYR_APPLY
+  return hipGetLastError();
+}
+
+}  // namespace fastqr

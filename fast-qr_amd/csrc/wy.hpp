@@ -1,0 +1,107 @@
+// wy.hpp — MFMA building blocks of the compact-WY trailing update (fp32,
+// v_mfma_f32_32x32x2f32), shared by the strip-resident update (qr_blocked.hip)
+// and the row-split update (qr_update.hip).
+//
+// A 32-row tile of one column strip is held in the MFMA accumulator layout:
+// lane (h = lane/32, l32 = lane%32) holds, in register 4q+i, row r0 + 8q + 4h + i
+// of column (strip start + l32).
+#pragma once
+
+#include "device.hpp"
+
+namespace fastqr {
+
+// Column-major matrix accessed through a buffer descriptor: element (row, col)
+// at byte offset 4 * (col * ldh + row); the host keeps 4 * ldh * n below 2^31,
+// so every offset fits in 32 bits.
+struct MatBuf {
+  rsrc_t r;
+  int ldh;
+  int n;
+  __device__ __forceinline__ uint32_t off(int row, int col) const { return 4u * (uint32_t)(col * ldh + row); }
+};
+
+// 32-row tile of column `col` (rows r0.., MFMA accumulator layout: register
+// 4q+i <- row r0 + 8q + 4h + i); rows >= n and !ok read as 0.
+template <bool VEC>
+__device__ __forceinline__ f32x16 tile_load(const MatBuf& M, int r0, int col, bool ok, int h) {
+  f32x16 x;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int rb = r0 + 8 * q + 4 * h;
+    if constexpr (VEC) {
+      const f32x4 v = buf_load4(M.r, (ok && rb < M.n) ? M.off(rb, col) : kOffNone);
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[4 * q + i] = v[i];
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) x[4 * q + i] = buf_load(M.r, (ok && rb + i < M.n) ? M.off(rb + i, col) : kOffNone);
+    }
+  }
+  return x;
+}
+
+template <bool VEC>
+__device__ __forceinline__ void tile_store(const MatBuf& M, int r0, int col, bool ok, int h, const f32x16& x) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int rb = r0 + 8 * q + 4 * h;
+    if constexpr (VEC) {
+      f32x4 v = {x[4 * q + 0], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]};
+      buf_store4(M.r, (ok && rb < M.n) ? M.off(rb, col) : kOffNone, v);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) buf_store(M.r, (ok && rb + i < M.n) ? M.off(rb + i, col) : kOffNone, x[4 * q + i]);
+    }
+  }
+}
+
+// P += V^T X for one 32-row tile at r0 of the transform whose reflectors start
+// at row/column kw (width nb).  V pattern A: lane holds rows r0 + 8q + 4h + i
+// of reflector l32, loaded 4 rows at a time.
+template <bool VEC>
+__device__ __forceinline__ void wy_accumulate(f32x16& P, const f32x16& X, const MatBuf& M, int kw, int nb, int r0,
+                                              int h, int l32) {
+  const int refl = l32;
+  const bool active = refl < nb;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int rb = r0 + 8 * q + 4 * h;
+    f32x4 v;
+    if constexpr (VEC) {
+      v = buf_load4(M.r, (active && rb < M.n) ? M.off(rb, kw + refl) : kOffNone);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = buf_load(M.r, (active && rb + i < M.n) ? M.off(rb + i, kw + refl) : kOffNone);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rr = rb + i - kw;  // row within the transform's panel
+      const float vv = (rr < refl) ? 0.0f : (rr == refl ? 1.0f : v[i]);
+      P = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, X[4 * q + i], P, 0, 0, 0);
+    }
+  }
+}
+
+// X += V W for one tile.  V pattern B: lane holds row r0 + l32 of reflector
+// 8q + 4h + i.
+__device__ __forceinline__ void wy_apply(f32x16& X, const f32x16& W, const MatBuf& M, int kw, int nb, int r0, int h,
+                                         int l32) {
+  const int row = r0 + l32;
+  const int rr = row - kw;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    float vb[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int refl = 8 * q + 4 * h + i;
+      const bool load = refl < nb && rr > refl && row < M.n;
+      const float v = buf_load(M.r, load ? M.off(row, kw + refl) : kOffNone);
+      vb[i] = (refl < nb && rr == refl) ? 1.0f : v;
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) X = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[i], W[4 * q + i], X, 0, 0, 0);
+  }
+}
+
+}  // namespace fastqr

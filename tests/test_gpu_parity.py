@@ -66,6 +66,20 @@ def test_blocked_path_matches_geqrf(cuda, n):
     assert_parity(a, h, tau)
 
 
+@pytest.mark.parametrize("batch,n", [(2, 1025), (1, 1100), (2, 1536), (1, 2047), (2, 2049), (1, 2050), (1, 3000)])
+def test_tall_matrices_match_geqrf(cuda, batch, n):
+    # tall matrices: n > 2048 takes the row-split trailing update (n = 2049 and
+    # 2050: partial strips and panels, scalar loads for odd n; n = 3000: panel
+    # width 16 above 2048 rows and 32 below in one factorisation); the smaller
+    # sizes cover the strip-resident update at its largest heights
+    _say(f"[tall] batch={batch} n={n}")
+    a = gaussian(batch, n, 600 + n)
+    h, tau = run_gpu(a, cuda)
+    assert h.stride() == (n * n, 1, n)
+    ag = assert_parity(a, h, tau)
+    _say(f"  {ag.message()}")
+
+
 @pytest.mark.parametrize("n", [32, 176, 512])
 def test_upper_triangular_input_is_left_unchanged(cuda, n):
     # known answer from the reference's tests (tests/test_qr_smoke.py:8078-8085):
