@@ -406,19 +406,19 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
         const double c = G.g_end - c0;
         err = timed(kUpdate, bd * 4.0 * m * wd * c, bd * (8.0 * m * c + 4.0 * m * wd), st, [&] {
           return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, pk, G.nb, G.slot_base + i, 1, c0, G.g_end,
-                                          vec, st);
+                                          vec, true, st);
         });
         if (err != hipSuccess) return err;
       }
     }
     return hipSuccess;
   };
-  auto run_update = [&](const Group& G, int c_begin, int c_end, hipStream_t st) -> hipError_t {
+  auto run_update = [&](const Group& G, int c_begin, int c_end, bool critical, hipStream_t st) -> hipError_t {
     if (c_end <= c_begin) return hipSuccess;
     const double m = ni - G.g0, wg = G.g_end - G.g0, c = c_end - c_begin;
     return timed(kUpdate, bd * 4.0 * m * wg * c, bd * (8.0 * m * c + 4.0 * m * wg), st, [&] {
       return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, G.g0, G.nb, G.slot_base, G.npan, c_begin,
-                                      c_end, vec, st);
+                                      c_end, vec, critical, st);
     });
   };
 
@@ -426,7 +426,7 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   if (!aux) {
     for (const Group& G : groups) {
       e = run_panels(G, stream);
-      if (e == hipSuccess) e = run_update(G, G.g_end, ni, stream);
+      if (e == hipSuccess) e = run_update(G, G.g_end, ni, false, stream);
       if (e != hipSuccess) return hip_fail(e, "blocked launch");
     }
     return FASTQR_OK;
@@ -444,12 +444,12 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
     const Group& Nx = groups[g + 1];
     hipEvent_t ev_next = aux->take(), ev_pan = aux->take();
     if (!ev_next || !ev_pan) return fail(FASTQR_EINVAL, "cannot create HIP events");
-    if ((e = run_update(G, Nx.g0, Nx.g_end, stream)) != hipSuccess) return hip_fail(e, "update launch");
+    if ((e = run_update(G, Nx.g0, Nx.g_end, true, stream)) != hipSuccess) return hip_fail(e, "update launch");
     if ((e = hipEventRecord(ev_next, stream)) != hipSuccess || (e = hipStreamWaitEvent(side, ev_next, 0)) != hipSuccess)
       return hip_fail(e, "stream join");
     if ((e = run_panels(Nx, side)) != hipSuccess) return hip_fail(e, "panel launch");
     if ((e = hipEventRecord(ev_pan, side)) != hipSuccess) return hip_fail(e, "stream join");
-    if ((e = run_update(G, Nx.g_end, ni, stream)) != hipSuccess) return hip_fail(e, "update launch");
+    if ((e = run_update(G, Nx.g_end, ni, false, stream)) != hipSuccess) return hip_fail(e, "update launch");
     if ((e = hipStreamWaitEvent(stream, ev_pan, 0)) != hipSuccess) return hip_fail(e, "stream join");
   }
   return FASTQR_OK;

@@ -29,7 +29,7 @@ hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float
 // Apply nwy compact-WY transforms (panels k0 + i*nb, T slots slot0 + i) to
 // columns [c_begin, c_end), rows [k0, n).
 hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n,
-                            int k0, int nb, int slot0, int nwy, int c_begin, int c_end, bool vec,
+                            int k0, int nb, int slot0, int nwy, int c_begin, int c_end, bool vec, bool hi_prio,
                             hipStream_t stream);
 
 // Row-split compact-WY update (qr_update.hip): for tall matrices and small

@@ -67,9 +67,12 @@ __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __re
 // operand, the contraction index permuted to match the accumulator layout),
 // P summed over waves in LDS, W = -(T^T P), X += V W.
 template <int NW, int TPW, bool RES, bool VEC>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(4, 8)))
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(TPW >= 4 && NW <= 8 ? 2 : 4, 8)))
 wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* __restrict__ Tws, int n, int k0,
-                 int nb, int slot0, int nwy, int c_begin, int c_end) {
+                 int nb, int slot0, int nwy, int c_begin, int c_end, int hi_prio) {
+  // updates on the critical path (the rest of a panel group, the next group's
+  // columns) win issue arbitration against the wide update they overlap
+  if (hi_prio) __builtin_amdgcn_s_setprio(2);
   const int64_t b = blockIdx.y;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -196,35 +199,67 @@ hipError_t launch_copy_colmajor(const float* A, int64_t batch, int n, int64_t as
 }
 
 hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n,
-                            int k0, int nb, int slot0, int nwy, int c_begin, int c_end, bool vec,
+                            int k0, int nb, int slot0, int nwy, int c_begin, int c_end, bool vec, bool hi_prio,
                             hipStream_t stream) {
   const int cols = c_end - c_begin;
   if (cols <= 0 || nwy <= 0) return hipSuccess;
   const int ntiles = (n - k0 + 31) / 32;
-  const dim3 grid((unsigned)((cols + 31) / 32), (unsigned)batch);
-#define FASTQR_WY(NW, TPW, RES)                                                                             \
-  do {                                                                                                      \
-    if (vec)                                                                                                \
-      hipLaunchKernelGGL((wy_update_kernel<NW, TPW, RES, true>), grid, dim3(NW * 64), 0, stream, H, hs0, ldh, \
-                         Tws, n, k0, nb, slot0, nwy, c_begin, c_end);                                       \
-    else                                                                                                    \
-      hipLaunchKernelGGL((wy_update_kernel<NW, TPW, RES, false>), grid, dim3(NW * 64), 0, stream, H, hs0,    \
-                         ldh, Tws, n, k0, nb, slot0, nwy, c_begin, c_end);                                  \
-  } while (0)
-  if (ntiles <= 4) {
-    FASTQR_WY(1, 4, true);
-  } else if (ntiles <= 8) {
-    FASTQR_WY(2, 4, true);
-  } else if (ntiles <= 16) {
-    FASTQR_WY(4, 4, true);
-  } else if (ntiles <= 32) {
-    FASTQR_WY(8, 4, true);
-  } else if (ntiles <= 64) {
-    FASTQR_WY(16, 4, true);
-  } else {
-    FASTQR_WY(16, 1, false);
+  const int64_t strips = (cols + 31) / 32;
+  const dim3 grid((unsigned)strips, (unsigned)batch);
+  // Tiles per wave: as few as the launch's size allows, so that a strip's
+  // MFMA work is spread over several SIMDs when there are few strips (small
+  // batches, narrow updates), and 4 per wave once the launch alone holds
+  // about four waves per SIMD of the GPU.
+  constexpr int64_t kWaveBudget = 4096;
+  int nw = 0, tpw = 0;
+  for (int t = 1; t <= 4; t *= 2) {
+    int w = 1;
+    while (w * t < ntiles) w *= 2;
+    if (w <= 16 && strips * batch * w <= kWaveBudget) {
+      nw = w, tpw = t;
+      break;
+    }
   }
+  if (nw == 0) {
+    tpw = 4;
+    nw = 1;
+    while (nw * 4 < ntiles && nw < 16) nw *= 2;
+  }
+  const bool res = nw * tpw >= ntiles;
+  const int prio = hi_prio ? 1 : 0;
+#define FASTQR_WY(NW, TPW, RES)                                                                                 \
+  if (nw == NW && tpw == TPW && res == RES) {                                                                   \
+    if (vec)                                                                                                    \
+      hipLaunchKernelGGL((wy_update_kernel<NW, TPW, RES, true>), grid, dim3(NW * 64), 0, stream, H, hs0, ldh,    \
+                         Tws, n, k0, nb, slot0, nwy, c_begin, c_end, prio);                                     \
+    else                                                                                                        \
+      hipLaunchKernelGGL((wy_update_kernel<NW, TPW, RES, false>), grid, dim3(NW * 64), 0, stream, H, hs0, ldh,   \
+                         Tws, n, k0, nb, slot0, nwy, c_begin, c_end, prio);                                     \
+    return hipGetLastError();                                                                                   \
+  }
+  FASTQR_WY(1, 1, true)
+  FASTQR_WY(2, 1, true)
+  FASTQR_WY(4, 1, true)
+  FASTQR_WY(8, 1, true)
+  FASTQR_WY(16, 1, true)
+  FASTQR_WY(1, 2, true)
+  FASTQR_WY(2, 2, true)
+  FASTQR_WY(4, 2, true)
+  FASTQR_WY(8, 2, true)
+  FASTQR_WY(16, 2, true)
+  FASTQR_WY(1, 4, true)
+  FASTQR_WY(2, 4, true)
+  FASTQR_WY(4, 4, true)
+  FASTQR_WY(8, 4, true)
+  FASTQR_WY(16, 4, true)
 #undef FASTQR_WY
+  // strips taller than 16 waves x 4 tiles: stream the tiles
+  if (vec)
+    hipLaunchKernelGGL((wy_update_kernel<16, 1, false, true>), grid, dim3(16 * 64), 0, stream, H, hs0, ldh, Tws, n,
+                       k0, nb, slot0, nwy, c_begin, c_end, prio);
+  else
+    hipLaunchKernelGGL((wy_update_kernel<16, 1, false, false>), grid, dim3(16 * 64), 0, stream, H, hs0, ldh, Tws, n,
+                       k0, nb, slot0, nwy, c_begin, c_end, prio);
   return hipGetLastError();
 }
 

@@ -103,13 +103,16 @@ __device__ __forceinline__ void wave_sync_lds() {
 // 16-column blocks.  VEC: rows are loaded and stored four at a time (m and the
 // leading dimension multiples of 4).
 template <int NW, int TPW, int NBLK, bool VEC>
-__global__ void __launch_bounds__(NW * 64) panel_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh,
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu((NW + 3) / 4, 8))) panel_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh,
                                                         float* __restrict__ tau, int64_t ts0, int64_t ts1,
                                                         float* __restrict__ Tws, int n, int k0, int slot) {
   static_assert(NW == 1 || NW % 2 == 0, "wave count");
   static_assert(NBLK == 1 || NBLK == 2, "16- or 32-column panels");
   static_assert(NW * TPW >= NBLK, "the panel's diagonal tiles must exist");
   constexpr int NB = 16 * NBLK;
+  // the panel is the critical path: its waves win issue arbitration against
+  // trailing-update waves running concurrently on the same SIMDs
+  __builtin_amdgcn_s_setprio(3);
   const int64_t b = blockIdx.x;
   const int m = n - k0;
   const int w = m < NB ? m : NB;
@@ -434,7 +437,7 @@ hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float
     } else if (m <= 512) {
       nw = 4, tpw = 8;
     } else if (m <= 1024) {
-      nw = 4, tpw = 16;
+      nw = 8, tpw = 8;
     } else if (m <= 2048) {
       nw = 8, tpw = 16;
     }
