@@ -293,11 +293,12 @@ void fastqr_debug_force_error(int code) { g_forced_error = code; }
 
 const char* fastqr_path_name(int64_t n) {
   if (n <= kWaveMaxN) return "wave64";
+  if (n <= fastqr::kLdsMaxN) return "lds";
   return "blocked";
 }
 
 size_t fastqr_workspace_bytes(int64_t batch, int64_t n) {
-  if (batch <= 0 || n <= kWaveMaxN || n > kMaxN) return 0;
+  if (batch <= 0 || n <= fastqr::kLdsMaxN || n > kMaxN) return 0;
   size_t floats = (size_t)batch * fastqr::kMaxSlots * 32 * 32;
   if (use_rowsplit(batch, n))
     floats += 2 * (size_t)batch * fastqr::kWyrTgStride + 2 * fastqr::wyr_workspace_floats(batch, (int)n);
@@ -329,18 +330,24 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   const hipStream_t stream = (hipStream_t)stream_ptr;
   const int ni = (int)n;
 
-  if (n <= kWaveMaxN) {
+  if (n <= fastqr::kLdsMaxN) {
+    // one workgroup (or wave) per matrix reads A once and writes H once: any H strides
     if (h_s1 == 0 || h_s2 == 0) return fail(FASTQR_ELAYOUT, "H strides must be non-zero");
     const bool same = (A == H && a_s0 == h_s0 && a_s1 == h_s1 && a_s2 == h_s2);
     if (!same && ranges_overlap(A, span_elems(batch, n, a_s0, a_s1, a_s2), H, span_elems(batch, n, h_s0, h_s1, h_s2)))
       return fail(FASTQR_EOVERLAP, "A and H overlap with different layouts");
     const double nn = (double)n;
-    const hipError_t e = timed(kWave, batch * 4.0 * nn * nn * nn / 3.0, batch * (8.0 * nn * nn + 4.0 * nn), stream,
-                               [&] {
-                                 return fastqr::launch_qr_wave(A, batch, ni, a_s0, a_s1, a_s2, H, h_s0, h_s1, h_s2,
-                                                               tau, tau_s0, tau_s1, stream);
-                               });
-    return e == hipSuccess ? FASTQR_OK : hip_fail(e, "qr_wave launch");
+    const double fl = batch * 4.0 * nn * nn * nn / 3.0, by = batch * (8.0 * nn * nn + 4.0 * nn);
+    if (n <= kWaveMaxN) {
+      const hipError_t e = timed(kWave, fl, by, stream, [&] {
+        return fastqr::launch_qr_wave(A, batch, ni, a_s0, a_s1, a_s2, H, h_s0, h_s1, h_s2, tau, tau_s0, tau_s1, stream);
+      });
+      return e == hipSuccess ? FASTQR_OK : hip_fail(e, "qr_wave launch");
+    }
+    const hipError_t e = timed(kLds, fl, by, stream, [&] {
+      return fastqr::launch_qr_lds(A, batch, ni, a_s0, a_s1, a_s2, H, h_s0, h_s1, h_s2, tau, tau_s0, tau_s1, stream);
+    });
+    return e == hipSuccess ? FASTQR_OK : hip_fail(e, "qr_lds launch");
   }
 
   // Blocked path: columns of H must be contiguous.

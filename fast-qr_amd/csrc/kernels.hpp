@@ -11,6 +11,12 @@ hipError_t launch_qr_wave(const float* A, int64_t batch, int n, int64_t as0, int
                           float* H, int64_t hs0, int64_t hs1, int64_t hs2, float* tau, int64_t ts0,
                           int64_t ts1, hipStream_t stream);
 
+// 64 < n <= kLdsMaxN: one workgroup per matrix, the matrix resident in LDS (qr_lds.hip).
+constexpr int kLdsMaxN = 176;
+hipError_t launch_qr_lds(const float* A, int64_t batch, int n, int64_t as0, int64_t as1, int64_t as2, float* H,
+                         int64_t hs0, int64_t hs1, int64_t hs2, float* tau, int64_t ts0, int64_t ts1,
+                         hipStream_t stream);
+
 // Blocked path (qr_blocked.hip).
 hipError_t launch_copy_colmajor(const float* A, int64_t batch, int n, int64_t as0, int64_t as1, int64_t as2,
                                 float* H, int64_t hs0, int64_t ldh, hipStream_t stream);

@@ -43,6 +43,12 @@ def assert_parity(a_cpu, h, tau, agree=True):
     return None
 
 
+def fastqr_path(n):
+    import fastqr
+
+    return fastqr.path_for(n)
+
+
 def gaussian(batch, n, seed):
     g = torch.Generator().manual_seed(seed)
     return torch.randn((batch, n, n), generator=g, dtype=torch.float32)
@@ -57,9 +63,11 @@ def test_wave_path_matches_geqrf(cuda, n):
     assert_parity(a, h, tau)
 
 
-@pytest.mark.parametrize("n", [65, 96, 100, 127, 128, 176, 200, 256, 352])
-def test_blocked_path_matches_geqrf(cuda, n):
-    _say(f"[blocked] n={n}")
+@pytest.mark.parametrize("n", [65, 67, 96, 100, 101, 127, 128, 150, 175, 176, 177, 200, 256, 352])
+def test_lds_and_blocked_paths_match_geqrf(cuda, n):
+    # 65..176: the LDS-resident path (odd n: rows padded to a multiple of 4);
+    # 177 and up: the blocked path
+    _say(f"[{fastqr_path(n)}] n={n}")
     a = gaussian(5, n, 200 + n)
     h, tau = run_gpu(a, cuda)
     assert h.stride() == (n * n, 1, n)
@@ -169,7 +177,22 @@ def test_forced_error_surfaces_as_exception(cuda):
     assert exc.value.code == -99
 
 
-@pytest.mark.parametrize("n", [48, 200])
+@pytest.mark.parametrize("n", [48, 150])
+def test_geqrf_into_row_major_h(cuda, n):
+    # the wave and LDS-resident paths write H with any strides
+    _say(f"[row-major H] n={n}")
+    import fastqr
+
+    a = gaussian(3, n, 700 + n)
+    h_ref, tau_ref = run_gpu(a, cuda)
+    h = torch.full((3, n, n), float("nan"), device=cuda)  # row-major
+    tau = torch.empty((3, n), device=cuda)
+    fastqr.geqrf_into(a.to(cuda), h, tau)
+    torch.cuda.synchronize()
+    assert torch.equal(h.cpu(), h_ref) and torch.equal(tau.cpu(), tau_ref)
+
+
+@pytest.mark.parametrize("n", [48, 150, 200])
 def test_geqrf_into_padded_leading_dimension(cuda, n):
     _say(f"[padded H] n={n}")
     import fastqr

@@ -43,7 +43,9 @@ def test_version_and_path_names():
     assert lib.fastqr_version() == 1
     assert lib.fastqr_path_name(1) == b"wave64"
     assert lib.fastqr_path_name(64) == b"wave64"
-    assert lib.fastqr_path_name(65) == b"blocked"
+    assert lib.fastqr_path_name(65) == b"lds"
+    assert lib.fastqr_path_name(176) == b"lds"
+    assert lib.fastqr_path_name(177) == b"blocked"
     assert fastqr.ext().version() == 1
     assert fastqr.path_for(4096) == "blocked"
 
@@ -51,6 +53,7 @@ def test_version_and_path_names():
 def test_workspace_bytes():
     lib = fastqr.cdll()
     assert lib.fastqr_workspace_bytes(20, 32) == 0  # wave path needs none
+    assert lib.fastqr_workspace_bytes(40, 176) == 0  # nor does the LDS-resident path
     assert lib.fastqr_workspace_bytes(0, 512) == 0
     small = lib.fastqr_workspace_bytes(1, 512)
     assert small > 0 and small % 256 == 0
@@ -76,11 +79,13 @@ def test_argument_validation_returns_codes_without_launching():
     assert _call(lib, A=0) == _lib.FASTQR_EINVAL
     assert b"non-null" in lib.fastqr_last_error()
     assert _call(lib, n=9000) == _lib.FASTQR_EINVAL
-    # blocked path needs contiguous columns of H
-    assert _call(lib, n=100, h_s=(10000, 100, 1)) == _lib.FASTQR_ELAYOUT
+    # blocked path needs contiguous columns of H and a workspace
+    assert _call(lib, n=200, h_s=(40000, 200, 1)) == _lib.FASTQR_ELAYOUT
     assert b"contiguous columns" in lib.fastqr_last_error()
-    assert _call(lib, n=100, ws_bytes=16) == _lib.FASTQR_EWORKSPACE
-    assert _call(lib, n=100, ws=0) == _lib.FASTQR_EWORKSPACE
+    assert _call(lib, n=200, ws_bytes=16) == _lib.FASTQR_EWORKSPACE
+    assert _call(lib, n=200, ws=0) == _lib.FASTQR_EWORKSPACE
+    # the LDS-resident path (n <= 176) takes any H strides and no workspace
+    # (the fake addresses are never dereferenced: only validation runs here)
     # A and H overlapping with different layouts
     assert _call(lib, n=100, A=16, a_s=(10000, 100, 1)) == _lib.FASTQR_EOVERLAP
     assert _call(lib, n=32, A=16, a_s=(1024, 32, 1)) == _lib.FASTQR_EOVERLAP
