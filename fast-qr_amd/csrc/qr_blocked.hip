@@ -59,7 +59,7 @@ __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __re
 // Applies `nwy` consecutive compact-WY transforms, transform i starting at
 // row and column kw = k0 + i*nb with width nb (<= 32) and T factor in
 // workspace slot (slot0 + i), to the 32-column strip
-// [c_begin + 32*blockIdx.x, +32) of [c_begin, c_end), rows [k0, n).  The strip
+// [c_begin + 32*strip, +32) of [c_begin, c_end), rows [k0, n).  The strip
 // is split into 32-row tiles; wave w owns tiles w, w+NW, ...  With RES the
 // tiles stay in VGPRs (MFMA accumulator layout) across all transforms: one
 // load and one store per element.  Without RES (taller strips) each transform
@@ -67,20 +67,28 @@ __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __re
 // operand, the contraction index permuted to match the accumulator layout),
 // P summed over waves in LDS, W = -(T^T P), X += V W.
 template <int NW, int TPW, bool RES, bool VEC>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu(TPW >= 4 && NW <= 8 ? 2 : 4, 8)))
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu((TPW >= 2 && NW == 8) || (TPW >= 4 && NW <= 8) ? 2 : 4, 8)))
 wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* __restrict__ Tws, int n, int k0,
-                 int nb, int slot0, int nwy, int c_begin, int c_end, int hi_prio) {
+                 int nb, int slot0, int nwy, int c_begin, int c_end, int hi_prio, int nstrips, int batch) {
   // updates on the critical path (the rest of a panel group, the next group's
   // columns) win issue arbitration against the wide update they overlap
   if (hi_prio) __builtin_amdgcn_s_setprio(2);
-  const int64_t b = blockIdx.y;
+  // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs, so
+  // workgroup L runs on XCD L % 8.  All strips of a matrix are given to one
+  // XCD (matrices xcd, xcd + 8, ... in turn), so the matrix's reflectors V,
+  // which every strip reads, are fetched into that XCD's L2 once.
+  const int L = blockIdx.x;
+  const int xk = L >> 3;
+  const int64_t b = (L & 7) + 8 * (xk / nstrips);
+  const int strip = xk % nstrips;
+  if (b >= batch) return;
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const int h = lane >> 5;
   const int l32 = lane & 31;
   const int m = n - k0;
   const int ntiles = (m + 31) >> 5;
-  const int col = c_begin + 32 * blockIdx.x + l32;
+  const int col = c_begin + 32 * strip + l32;
   const bool colok = col < c_end;
   const MatBuf M{make_rsrc(H + b * hs0, (uint32_t)(4 * ldh * n)), (int)ldh, n};
 
@@ -114,12 +122,29 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
     f32x16 P;
 #pragma unroll
     for (int j = 0; j < 16; ++j) P[j] = 0.0f;
-    if constexpr (RES) {
+    // Software-pipelined V loads cost a second tile of V in registers.  They
+    // pay off with 8 waves per workgroup (tall strips); with 16 waves there is
+    // no room for them, and the 4-wave variants (short strips, many
+    // workgroups) gain more from the occupancy the registers would cost.
+    constexpr bool PF = NW == 8 || TPW == 1;
+    if constexpr (RES && !PF) {
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const int rt = wave + NW * t;
         if (rt < ntiles && rt >= rt_first) wy_accumulate<VEC>(P, X[t], M, kw, nb, kb + 32 * rt, h, l32);
-        __builtin_amdgcn_sched_barrier(0);  // keep each tile's V loads next to its MFMAs
+        __builtin_amdgcn_sched_barrier(0);
+      }
+    } else if constexpr (RES) {
+      // V loads of tile t+1 are issued before the MFMAs of tile t
+      f32x16 va = wy_load_va<VEC>(M, kw, nb, kb + 32 * wave, h, l32, wave < ntiles && wave >= rt_first);
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const int rt = wave + NW * t;
+        f32x16 va_next;
+        if (t + 1 < TPW)
+          va_next = wy_load_va<VEC>(M, kw, nb, kb + 32 * (rt + NW), h, l32, rt + NW < ntiles && rt + NW >= rt_first);
+        if (rt < ntiles && rt >= rt_first) wy_mfma_p(P, va, X[t]);
+        if (t + 1 < TPW) va = va_next;
       }
     } else {
       for (int rt = wave; rt < ntiles; rt += NW) {
@@ -156,12 +181,23 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
     }
 #pragma unroll
     for (int j = 0; j < 16; ++j) W[j] = -W[j];
-    if constexpr (RES) {
+    if constexpr (RES && !PF) {
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const int rt = wave + NW * t;
         if (rt < ntiles && rt >= rt_first) wy_apply(X[t], W, M, kw, nb, kb + 32 * rt, h, l32);
         __builtin_amdgcn_sched_barrier(0);
+      }
+    } else if constexpr (RES) {
+      f32x16 vb = wy_load_vb(M, kw, nb, kb + 32 * wave, h, l32, wave < ntiles && wave >= rt_first);
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const int rt = wave + NW * t;
+        f32x16 vb_next;
+        if (t + 1 < TPW)
+          vb_next = wy_load_vb(M, kw, nb, kb + 32 * (rt + NW), h, l32, rt + NW < ntiles && rt + NW >= rt_first);
+        if (rt < ntiles && rt >= rt_first) wy_mfma_apply(X[t], vb, W);
+        if (t + 1 < TPW) vb = vb_next;
       }
     } else {
       for (int rt = wave; rt < ntiles; rt += NW) {
@@ -205,7 +241,10 @@ hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, c
   if (cols <= 0 || nwy <= 0) return hipSuccess;
   const int ntiles = (n - k0 + 31) / 32;
   const int64_t strips = (cols + 31) / 32;
-  const dim3 grid((unsigned)strips, (unsigned)batch);
+  const int64_t groups8 = (batch + 7) / 8;
+  if (8 * groups8 * strips > 0x7fffffffLL) return hipErrorInvalidValue;
+  const dim3 grid((unsigned)(8 * groups8 * strips));
+  const int ns = (int)strips, nbatch = (int)batch;
   // Tiles per wave: as few as the launch's size allows, so that a strip's
   // MFMA work is spread over several SIMDs when there are few strips (small
   // batches, narrow updates), and 4 per wave once the launch alone holds
@@ -231,10 +270,10 @@ hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, c
   if (nw == NW && tpw == TPW && res == RES) {                                                                   \
     if (vec)                                                                                                    \
       hipLaunchKernelGGL((wy_update_kernel<NW, TPW, RES, true>), grid, dim3(NW * 64), 0, stream, H, hs0, ldh,    \
-                         Tws, n, k0, nb, slot0, nwy, c_begin, c_end, prio);                                     \
+                         Tws, n, k0, nb, slot0, nwy, c_begin, c_end, prio, ns, nbatch);                                     \
     else                                                                                                        \
       hipLaunchKernelGGL((wy_update_kernel<NW, TPW, RES, false>), grid, dim3(NW * 64), 0, stream, H, hs0, ldh,   \
-                         Tws, n, k0, nb, slot0, nwy, c_begin, c_end, prio);                                     \
+                         Tws, n, k0, nb, slot0, nwy, c_begin, c_end, prio, ns, nbatch);                                     \
     return hipGetLastError();                                                                                   \
   }
   FASTQR_WY(1, 1, true)
@@ -256,10 +295,10 @@ hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, c
   // strips taller than 16 waves x 4 tiles: stream the tiles
   if (vec)
     hipLaunchKernelGGL((wy_update_kernel<16, 1, false, true>), grid, dim3(16 * 64), 0, stream, H, hs0, ldh, Tws, n,
-                       k0, nb, slot0, nwy, c_begin, c_end, prio);
+                       k0, nb, slot0, nwy, c_begin, c_end, prio, ns, nbatch);
   else
     hipLaunchKernelGGL((wy_update_kernel<16, 1, false, false>), grid, dim3(16 * 64), 0, stream, H, hs0, ldh, Tws, n,
-                       k0, nb, slot0, nwy, c_begin, c_end, prio);
+                       k0, nb, slot0, nwy, c_begin, c_end, prio, ns, nbatch);
   return hipGetLastError();
 }
 

@@ -104,4 +104,56 @@ __device__ __forceinline__ void wy_apply(f32x16& X, const f32x16& W, const MatBu
   }
 }
 
+// Split forms of wy_accumulate / wy_apply for software pipelining: the V
+// values of a tile are loaded (with the unit diagonal and the zeros above it
+// applied) into registers first, so a caller can issue the loads of the next
+// tile before the MFMAs of the current one.  `ok` false loads zeros.
+template <bool VEC>
+__device__ __forceinline__ f32x16 wy_load_va(const MatBuf& M, int kw, int nb, int r0, int h, int l32, bool ok) {
+  const int refl = l32;
+  const bool active = ok && refl < nb;
+  f32x16 va;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+    const int rb = r0 + 8 * q + 4 * h;
+    f32x4 v;
+    if constexpr (VEC) {
+      v = buf_load4(M.r, (active && rb < M.n) ? M.off(rb, kw + refl) : kOffNone);
+    } else {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) v[i] = buf_load(M.r, (active && rb + i < M.n) ? M.off(rb + i, kw + refl) : kOffNone);
+    }
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int rr = rb + i - kw;
+      va[4 * q + i] = (rr < refl) ? 0.0f : (rr == refl ? 1.0f : v[i]);
+    }
+  }
+  return va;
+}
+
+__device__ __forceinline__ void wy_mfma_p(f32x16& P, const f32x16& va, const f32x16& X) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) P = __builtin_amdgcn_mfma_f32_32x32x2f32(va[j], X[j], P, 0, 0, 0);
+}
+
+__device__ __forceinline__ f32x16 wy_load_vb(const MatBuf& M, int kw, int nb, int r0, int h, int l32, bool ok) {
+  const int row = r0 + l32;
+  const int rr = row - kw;
+  f32x16 vb;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) {
+    const int refl = 8 * (j >> 2) + 4 * h + (j & 3);
+    const bool load = ok && refl < nb && rr > refl && row < M.n;
+    const float v = buf_load(M.r, load ? M.off(row, kw + refl) : kOffNone);
+    vb[j] = (refl < nb && rr == refl) ? 1.0f : v;
+  }
+  return vb;
+}
+
+__device__ __forceinline__ void wy_mfma_apply(f32x16& X, const f32x16& vb, const f32x16& W) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) X = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[j], W[j], X, 0, 0, 0);
+}
+
 }  // namespace fastqr
