@@ -61,7 +61,101 @@ def parse_args():
                    help="target CPU seconds per shape for the torch.geqrf baseline (0 disables)")
     p.add_argument("--no-check", action="store_true", help="skip the post-timing recheck")
     p.add_argument("--no-profile", action="store_true", help="skip the instrumented per-kernel pass")
+    p.add_argument("--calibrate-copy", action="store_true",
+                   help="start with a plain 256 MiB device copy (the reference kernel for HBM counter scaling)")
+    p.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
+                   help="print the HBM traffic summary of two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
+                        "this script with --calibrate-copy, and exit")
+    p.add_argument("--traffic-file", default=str(ROOT / "profiles" / TRAFFIC_SUMMARY),
+                   help="committed traffic summary that fills roofline.traffic")
     return p.parse_args()
+
+
+# ---- HBM traffic from rocprofv3 counters ---------------------------------------
+TRAFFIC_SUMMARY = "hbm_traffic_bench_all_workloads.md"
+CALIB_BYTES = 256 * 1024 * 1024
+KIND_OF = (("panel_kernel", "panel"), ("wy_update_kernel", "update"), ("wyr_", "update_rowsplit"),
+           ("copy_to_colmajor", "copy"), ("qr_wave_kernel", "wave64"), ("qr_lds_kernel", "lds"))
+
+
+def _counter_rows(directory: str, counter: str):
+    """(kernel name, KiB) per dispatch, in dispatch order, from a rocprofv3 --pmc csv."""
+    import csv
+    import glob
+
+    paths = glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True)
+    if not paths:
+        raise SystemExit(f"no counter_collection.csv under {directory}")
+    per = {}
+    order = []
+    for row in csv.DictReader(open(paths[0])):
+        if row["Counter_Name"] != counter:
+            continue
+        d = row["Dispatch_Id"]
+        if d not in per:
+            per[d] = [row["Kernel_Name"], 0.0]
+            order.append(d)
+        per[d][1] += float(row["Counter_Value"])
+    return [per[d] for d in order]
+
+
+def summarize_traffic(fetch_dir: str, write_dir: str) -> str:
+    """Markdown summary: per kernel kind, calibrated HBM bytes per launch."""
+    out = {}
+    factors = {}
+    for counter, directory in (("FETCH_SIZE", fetch_dir), ("WRITE_SIZE", write_dir)):
+        rows = _counter_rows(directory, counter)
+        calib = [kib for name, kib in rows if "copyBuffer" in name]
+        if not calib:
+            raise SystemExit(f"{directory}: no copy kernel to calibrate against (run with --calibrate-copy)")
+        factor = CALIB_BYTES / (calib[0] * 1024.0)  # true bytes per counted byte
+        factors[counter] = factor
+        for name, kib in rows:
+            kind = next((k for key, k in KIND_OF if key in name), None)
+            if kind is None or "fastqr" not in name:
+                continue
+            ent = out.setdefault(kind, {"FETCH_SIZE": [0, 0.0], "WRITE_SIZE": [0, 0.0]})
+            ent[counter][0] += 1
+            ent[counter][1] += kib * 1024.0 * factor
+    lines = [
+        "# HBM traffic per launch — bench.py, all five workloads (one timed step)",
+        "",
+        "Commands (repository root on one MI355X; `$REPO` is the repository root):",
+        "",
+        "```",
+        "cd /tmp && rocprofv3 --pmc FETCH_SIZE -d $REPO/gpurun_out/pmc_bfetch -o run -f csv -- python3 $REPO/bench.py "
+        "--steps 1 --warmup 0 --no-profile --no-check --cpu-sample-seconds 0 --calibrate-copy",
+        "cd /tmp && rocprofv3 --pmc WRITE_SIZE -d $REPO/gpurun_out/pmc_bwrite -o run -f csv -- python3 $REPO/bench.py "
+        "--steps 1 --warmup 0 --no-profile --no-check --cpu-sample-seconds 0 --calibrate-copy",
+        "python3 bench.py --summarize-traffic gpurun_out/pmc_bfetch gpurun_out/pmc_bwrite",
+        "```",
+        "",
+        "Calibration: a plain 256 MiB device copy (`__amd_rocclr_copyBuffer`) in the same run; each counter is "
+        "scaled by (256 MiB / what it reads for that copy): FETCH_SIZE x%.3f, WRITE_SIZE x%.3f."
+        % (factors["FETCH_SIZE"], factors["WRITE_SIZE"]),
+        "",
+        "| kernel kind | launches | fetch MiB/launch | write MiB/launch | HBM bytes/launch |",
+        "|---|---:|---:|---:|---:|",
+    ]
+    for kind, ent in sorted(out.items()):
+        n = max(ent["FETCH_SIZE"][0], 1)
+        fb = ent["FETCH_SIZE"][1] / n
+        wb = ent["WRITE_SIZE"][1] / max(ent["WRITE_SIZE"][0], 1)
+        lines.append(f"| {kind} | {n} | {fb / 2**20:.2f} | {wb / 2**20:.2f} | {fb + wb:.6g} |")
+    lines.append("")
+    return "\n".join(lines)
+
+
+def traffic_per_launch(path: str, kind: str):
+    """HBM bytes per launch of `kind` from a committed summary, or None."""
+    try:
+        for line in open(path):
+            cells = [c.strip() for c in line.strip().strip("|").split("|")]
+            if len(cells) == 5 and cells[0] == kind:
+                return float(cells[4])
+    except (OSError, ValueError):
+        return None
+    return None
 
 
 def count_for(batch: int, n: int) -> int:
@@ -76,6 +170,9 @@ def geomean(xs):
 
 def main() -> int:
     args = parse_args()
+    if args.summarize_traffic:
+        print(summarize_traffic(*args.summarize_traffic))
+        return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world > 1:
         log("bench.py measures one GPU only: every matrix is independent, so the path shards by batch "
@@ -96,6 +193,12 @@ def main() -> int:
     ncores = len(os.sched_getaffinity(0))
     torch.set_num_threads(ncores)
     fastqr.ext()  # fail loudly if the native library is missing
+    if args.calibrate_copy:
+        src = torch.ones(CALIB_BYTES // 4, device=dev)
+        dst = torch.empty_like(src)
+        dst.copy_(src)
+        torch.cuda.synchronize()
+        del src, dst
 
     names = [c.strip() for c in args.configs.split(",") if c.strip()]
     shapes = [(name, s) for name in names for s in inputs.WORKLOADS[name]]
@@ -230,8 +333,9 @@ def main() -> int:
                 tot_ms = sum(st["ms"] for st in kernels[s.label].values())
                 for kname in kk:
                     kk[kname]["share"] = round(kernels[s.label][kname]["ms"] / tot_ms, 3) if tot_ms else None
-                if "update" in kk and kk["update"]["tflops"] is not None:
-                    kk["update"]["pct_fp32_mfma_peak"] = round(100 * kk["update"]["tflops"] / PEAK_FP32_TFLOPS, 2)
+                for uk in ("update", "update_rowsplit"):
+                    if uk in kk and kk[uk]["tflops"] is not None:
+                        kk[uk]["pct_fp32_mfma_peak"] = round(100 * kk[uk]["tflops"] / PEAK_FP32_TFLOPS, 2)
                 row["kernels"] = kk
             if s.label in cpu:
                 row["cpu_geqrf_us"] = round(cpu[s.label]["us_per_call"], 1)
@@ -256,20 +360,22 @@ def main() -> int:
         for label, kd in kernels.items():
             for kname, st in kd.items():
                 per_kind_ms[kname] = per_kind_ms.get(kname, 0.0) + st["ms"]
-            st = kd["update"]
+            st = kd.get("update", {})
             for f in agg:
-                agg[f] += st[f]
+                agg[f] += st.get(f, 0)
         if agg["launches"] and agg["ms"] > 0:
             avg_s = agg["ms"] * 1e-3 / agg["launches"]
             achieved = agg["flops"] / agg["launches"] / avg_s / 1e12
             roof = {
                 "bound": "mfma",
-                "kernel": "update_kernel (A2 -= V T^T V^T A2, v_mfma_f32_32x32x2f32)",
+                "kernel": "wy_update_kernel (trailing update A2 -= V T^T V^T A2, v_mfma_f32_32x32x2f32), "
+                          "all launches of all workloads",
                 "achieved": round(achieved, 2),
                 "peak": PEAK_FP32_TFLOPS,
                 "unit": "TFLOP/s",
                 "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
-                "traffic": None,
+                "traffic": traffic_per_launch(args.traffic_file, "update"),
+                "traffic_source": os.path.relpath(args.traffic_file, ROOT),
                 "launches": agg["launches"],
                 "avg_launch_us": round(avg_s * 1e6, 3),
                 "flops_per_launch": agg["flops"] / agg["launches"],

@@ -53,8 +53,8 @@ int64_t span_elems(int64_t batch, int64_t n, int64_t s0, int64_t s1, int64_t s2)
 }
 
 // ---- opt-in per-launch profiling (fastqr_profile_*) ----------------------
-enum Kind { kCopy = 0, kPanel = 1, kUpdate = 2, kWave = 3, kLds = 4 };
-const char* const kKindNames[FASTQR_PROFILE_KINDS] = {"copy", "panel", "update", "wave64", "lds"};
+enum Kind { kCopy = 0, kPanel = 1, kUpdate = 2, kWave = 3, kLds = 4, kUpdateRows = 5 };
+const char* const kKindNames[FASTQR_PROFILE_KINDS] = {"copy", "panel", "update", "wave64", "lds", "update_rowsplit"};
 
 struct Record {
   int kind;
@@ -208,7 +208,7 @@ int run_rowsplit(float* H, int64_t batch, int64_t hs0, int64_t ldh, float* tau, 
   auto run_wyr = [&](const WyrCall& c, hipStream_t st) -> hipError_t {
     const double m = n - c.kv, k = c.k;
     const double cx = c.c_end - c.c_begin - (c.gram ? 32.0 * ((c.k + 31) / 32) : 0.0);
-    return timed(kUpdate, bd * 4.0 * m * k * cx, bd * (12.0 * m * cx + 8.0 * m * k), st,
+    return timed(kUpdateRows, bd * 4.0 * m * k * cx, bd * (12.0 * m * cx + 8.0 * m * k), st,
                  [&] { return fastqr::launch_wyr(c, st); });
   };
 

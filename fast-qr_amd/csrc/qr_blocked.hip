@@ -23,7 +23,7 @@ namespace fastqr {
 __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __restrict__ A, int64_t as0,
                                                                 int64_t as1, int64_t as2,
                                                                 float* __restrict__ H, int64_t hs0,
-                                                                int64_t ldh, int n, int ntile) {
+                                                                int64_t ldh, int n, int ntile, bool vec) {
   __shared__ float tile[64][65];
   const int64_t b = blockIdx.y;
   const int ti = blockIdx.x % ntile;
@@ -31,6 +31,35 @@ __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __re
   const float* Ab = A + b * as0;
   float* Hb = H + b * hs0;
   const int tid = threadIdx.x;
+  if (vec) {
+    // row-major source, every row and column a multiple of 16 bytes: each
+    // thread moves four 16-byte row segments in and four column segments out
+    const int c4 = 4 * (tid & 15);
+    f32x4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = (tid >> 4) + 16 * k;
+      const int gi = ti * 64 + i, gj = tj * 64 + c4;
+      v[k] = (gi < n && gj < n) ? *reinterpret_cast<const f32x4*>(Ab + (int64_t)gi * as1 + gj)
+                                : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int i = (tid >> 4) + 16 * k;
+#pragma unroll
+      for (int e = 0; e < 4; ++e) tile[i][c4 + e] = v[k][e];
+    }
+    __syncthreads();
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int j = (tid >> 4) + 16 * k;
+      const int gi = ti * 64 + c4, gj = tj * 64 + j;
+      if (gi < n && gj < n)
+        *reinterpret_cast<f32x4*>(Hb + (int64_t)gj * ldh + gi) =
+            f32x4{tile[c4][j], tile[c4 + 1][j], tile[c4 + 2][j], tile[c4 + 3][j]};
+    }
+    return;
+  }
   if (as1 != 1) {
     // consecutive threads walk along j (row-major-like source)
     for (int idx = tid; idx < 64 * 64; idx += 256) {
@@ -67,7 +96,7 @@ __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __re
 // operand, the contraction index permuted to match the accumulator layout),
 // P summed over waves in LDS, W = -(T^T P), X += V W.
 template <int NW, int TPW, bool RES, bool VEC>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu((TPW >= 2 && NW == 8) || (TPW >= 4 && NW <= 8) ? 2 : 4, 8)))
+__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu((TPW >= 2 && NW == 8) || (TPW >= 4 && NW <= 4) ? 2 : 4, 8)))
 wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* __restrict__ Tws, int n, int k0,
                  int nb, int slot0, int nwy, int c_begin, int c_end, int hi_prio, int nstrips, int batch) {
   // updates on the critical path (the rest of a panel group, the next group's
@@ -122,12 +151,17 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
     f32x16 P;
 #pragma unroll
     for (int j = 0; j < 16; ++j) P[j] = 0.0f;
-    // Software-pipelined V loads cost a second tile of V in registers.  They
-    // pay off with 8 waves per workgroup (tall strips); with 16 waves there is
-    // no room for them, and the 4-wave variants (short strips, many
-    // workgroups) gain more from the occupancy the registers would cost.
-    constexpr bool PF = NW == 8 || TPW == 1;
-    if constexpr (RES && !PF) {
+    // V prefetch depth: 0 = each tile's V loads next to its MFMAs, 2 = the V
+    // of all of this wave's tiles in flight at once (pattern A before the
+    // P MFMAs, pattern B before the reduction of P over the waves), at the
+    // cost of TPW more tiles of registers.  Measured on MI355X: it pays with
+    // 8 waves per workgroup (tall strips, few workgroups per CU); the 4-wave
+    // variants (short strips, many workgroups) gain more from the occupancy
+    // the registers would cost, and 16 waves (128 registers each) leave no
+    // room for it.
+    constexpr int PFM = (RES && TPW > 1 && NW == 8) ? 2 : 0;
+    f32x16 vb[PFM == 2 ? TPW : 1];
+    if constexpr (RES && PFM == 0) {
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const int rt = wave + NW * t;
@@ -135,16 +169,21 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
         __builtin_amdgcn_sched_barrier(0);
       }
     } else if constexpr (RES) {
-      // V loads of tile t+1 are issued before the MFMAs of tile t
-      f32x16 va = wy_load_va<VEC>(M, kw, nb, kb + 32 * wave, h, l32, wave < ntiles && wave >= rt_first);
+      f32x16 va[TPW];
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const int rt = wave + NW * t;
-        f32x16 va_next;
-        if (t + 1 < TPW)
-          va_next = wy_load_va<VEC>(M, kw, nb, kb + 32 * (rt + NW), h, l32, rt + NW < ntiles && rt + NW >= rt_first);
-        if (rt < ntiles && rt >= rt_first) wy_mfma_p(P, va, X[t]);
-        if (t + 1 < TPW) va = va_next;
+        va[t] = wy_load_va<VEC>(M, kw, nb, kb + 32 * rt, h, l32, rt < ntiles && rt >= rt_first);
+      }
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const int rt = wave + NW * t;
+        if (rt < ntiles && rt >= rt_first) wy_mfma_p(P, va[t], X[t]);
+      }
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const int rt = wave + NW * t;
+        vb[t] = wy_load_vb(M, kw, nb, kb + 32 * rt, h, l32, rt < ntiles && rt >= rt_first);
       }
     } else {
       for (int rt = wave; rt < ntiles; rt += NW) {
@@ -181,7 +220,7 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
     }
 #pragma unroll
     for (int j = 0; j < 16; ++j) W[j] = -W[j];
-    if constexpr (RES && !PF) {
+    if constexpr (RES && PFM == 0) {
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const int rt = wave + NW * t;
@@ -189,15 +228,10 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
         __builtin_amdgcn_sched_barrier(0);
       }
     } else if constexpr (RES) {
-      f32x16 vb = wy_load_vb(M, kw, nb, kb + 32 * wave, h, l32, wave < ntiles && wave >= rt_first);
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const int rt = wave + NW * t;
-        f32x16 vb_next;
-        if (t + 1 < TPW)
-          vb_next = wy_load_vb(M, kw, nb, kb + 32 * (rt + NW), h, l32, rt + NW < ntiles && rt + NW >= rt_first);
-        if (rt < ntiles && rt >= rt_first) wy_mfma_apply(X[t], vb, W);
-        if (t + 1 < TPW) vb = vb_next;
+        if (rt < ntiles && rt >= rt_first) wy_mfma_apply(X[t], vb[t], W);
       }
     } else {
       for (int rt = wave; rt < ntiles; rt += NW) {
@@ -229,8 +263,10 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
 hipError_t launch_copy_colmajor(const float* A, int64_t batch, int n, int64_t as0, int64_t as1, int64_t as2,
                                 float* H, int64_t hs0, int64_t ldh, hipStream_t stream) {
   const int ntile = (n + 63) / 64;
+  const bool vec = as2 == 1 && (as1 & 3) == 0 && (as0 & 3) == 0 && ((uintptr_t)A & 15) == 0 && (ldh & 3) == 0 &&
+                   (hs0 & 3) == 0 && ((uintptr_t)H & 15) == 0 && (n & 3) == 0;
   hipLaunchKernelGGL(copy_to_colmajor_kernel, dim3(ntile * ntile, (unsigned)batch), dim3(256), 0, stream, A,
-                     as0, as1, as2, H, hs0, ldh, n, ntile);
+                     as0, as1, as2, H, hs0, ldh, n, ntile, vec);
   return hipGetLastError();
 }
 

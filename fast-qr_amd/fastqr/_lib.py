@@ -35,7 +35,7 @@ EXPORTED_SYMBOLS = (
     "fastqr_profile_collect",
     "fastqr_profile_kind_name",
 )
-PROFILE_KINDS = ("copy", "panel", "update", "wave64", "lds")
+PROFILE_KINDS = ("copy", "panel", "update", "wave64", "lds", "update_rowsplit")
 
 
 class FastQRUnavailable(RuntimeError):

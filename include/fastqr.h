@@ -113,9 +113,12 @@ void fastqr_debug_force_error(int code);
  * fastqr_profile_collect(kind, ...)  waits for the recorded events and returns
  *   launch count, summed kernel milliseconds, and summed algorithmic flops and
  *   bytes for kind `kind` (0 .. FASTQR_PROFILE_KINDS-1); returns 0 or a status.
- * fastqr_profile_kind_name(kind)  "copy", "panel", "update", "wave64", "lds".
+ * fastqr_profile_kind_name(kind)  "copy", "panel", "update" (the strip-resident
+ *   trailing update, one kernel per launch), "wave64", "lds", "update_rowsplit"
+ *   (the row-split trailing update of tall matrices: one record per call of
+ *   its partial-product / T / W / apply kernel sequence).
  */
-#define FASTQR_PROFILE_KINDS 5
+#define FASTQR_PROFILE_KINDS 6
 int fastqr_profile_enable(int on);
 int fastqr_profile_collect(int kind, int64_t* launches, double* milliseconds, double* flops, double* bytes);
 const char* fastqr_profile_kind_name(int kind);
