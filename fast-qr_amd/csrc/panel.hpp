@@ -118,7 +118,7 @@ __device__ __forceinline__ void panel_body(IO& io, int m, int tid) {
   constexpr int NB = 16 * NBLK;
   const int w = m < NB ? m : NB;
   const int lane = tid & 63;
-  const int wave = NW == 1 ? 0 : (tid >> 6);
+  const int wave = NW == 1 ? 0 : __builtin_amdgcn_readfirstlane(tid >> 6);
   const int kq = lane >> 4;
   const int cn = lane & 15;
 

@@ -112,7 +112,7 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
   const int strip = xk % nstrips;
   if (b >= batch) return;
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar branches on tiles
   const int h = lane >> 5;
   const int l32 = lane & 31;
   const int m = n - k0;

@@ -242,7 +242,7 @@ __global__ void __launch_bounds__(kLdsWaves * 64) qr_lds_kernel(const float* __r
       panel_body<1, 4, 2, true>(io, m, t);
     }
     __syncthreads();
-    if (w == 32) lds_update(M, ldm, n, npad, k0, Tk, t >> 6, (t >> 5) & 1, t & 31);
+    if (w == 32) lds_update(M, ldm, n, npad, k0, Tk, __builtin_amdgcn_readfirstlane(t >> 6), (t >> 5) & 1, t & 31);
     __syncthreads();
   }
 

@@ -56,63 +56,35 @@ __device__ __forceinline__ void tile_store(const MatBuf& M, int r0, int col, boo
   }
 }
 
-// P += V^T X for one 32-row tile at r0 of the transform whose reflectors start
-// at row/column kw (width nb).  V pattern A: lane holds rows r0 + 8q + 4h + i
-// of reflector l32, loaded 4 rows at a time.
-template <bool VEC>
-__device__ __forceinline__ void wy_accumulate(f32x16& P, const f32x16& X, const MatBuf& M, int kw, int nb, int r0,
-                                              int h, int l32) {
-  const int refl = l32;
-  const bool active = refl < nb;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    const int rb = r0 + 8 * q + 4 * h;
-    f32x4 v;
-    if constexpr (VEC) {
-      v = buf_load4(M.r, (active && rb < M.n) ? M.off(rb, kw + refl) : kOffNone);
-    } else {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) v[i] = buf_load(M.r, (active && rb + i < M.n) ? M.off(rb + i, kw + refl) : kOffNone);
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int rr = rb + i - kw;  // row within the transform's panel
-      const float vv = (rr < refl) ? 0.0f : (rr == refl ? 1.0f : v[i]);
-      P = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, X[4 * q + i], P, 0, 0, 0);
-    }
-  }
-}
-
-// X += V W for one tile.  V pattern B: lane holds row r0 + l32 of reflector
-// 8q + 4h + i.
-__device__ __forceinline__ void wy_apply(f32x16& X, const f32x16& W, const MatBuf& M, int kw, int nb, int r0, int h,
-                                         int l32) {
-  const int row = r0 + l32;
-  const int rr = row - kw;
-#pragma unroll
-  for (int q = 0; q < 4; ++q) {
-    float vb[4];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      const int refl = 8 * q + 4 * h + i;
-      const bool load = refl < nb && rr > refl && row < M.n;
-      const float v = buf_load(M.r, load ? M.off(row, kw + refl) : kOffNone);
-      vb[i] = (refl < nb && rr == refl) ? 1.0f : v;
-    }
-#pragma unroll
-    for (int i = 0; i < 4; ++i) X = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[i], W[4 * q + i], X, 0, 0, 0);
-  }
-}
-
-// Split forms of wy_accumulate / wy_apply for software pipelining: the V
-// values of a tile are loaded (with the unit diagonal and the zeros above it
-// applied) into registers first, so a caller can issue the loads of the next
-// tile before the MFMAs of the current one.  `ok` false loads zeros.
+// V of the transform whose reflectors start at row/column kw (width nb <= 32)
+// for the 32-row tile at r0, with the unit diagonal and the zeros above it
+// applied; `ok` false loads zeros.
+//   pattern A (P = V^T X): lane holds rows r0 + 8q + 4h + i of reflector l32;
+//   pattern B (X += V W):  lane holds row r0 + l32 of reflector 8q + 4h + i.
+// Only a tile that starts above row kw + nb meets the triangle; every other
+// tile (and, for nb = 32, every reflector index) needs no per-element mask,
+// which the uniform branches below exploit.
 template <bool VEC>
 __device__ __forceinline__ f32x16 wy_load_va(const MatBuf& M, int kw, int nb, int r0, int h, int l32, bool ok) {
   const int refl = l32;
-  const bool active = ok && refl < nb;
   f32x16 va;
+  if (r0 >= kw + nb && nb == 32) {
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int rb = r0 + 8 * q + 4 * h;
+      f32x4 v;
+      if constexpr (VEC) {
+        v = buf_load4(M.r, (ok && rb < M.n) ? M.off(rb, kw + refl) : kOffNone);
+      } else {
+#pragma unroll
+        for (int i = 0; i < 4; ++i) v[i] = buf_load(M.r, (ok && rb + i < M.n) ? M.off(rb + i, kw + refl) : kOffNone);
+      }
+#pragma unroll
+      for (int i = 0; i < 4; ++i) va[4 * q + i] = v[i];
+    }
+    return va;
+  }
+  const bool active = ok && refl < nb;
 #pragma unroll
   for (int q = 0; q < 4; ++q) {
     const int rb = r0 + 8 * q + 4 * h;
@@ -132,15 +104,19 @@ __device__ __forceinline__ f32x16 wy_load_va(const MatBuf& M, int kw, int nb, in
   return va;
 }
 
-__device__ __forceinline__ void wy_mfma_p(f32x16& P, const f32x16& va, const f32x16& X) {
-#pragma unroll
-  for (int j = 0; j < 16; ++j) P = __builtin_amdgcn_mfma_f32_32x32x2f32(va[j], X[j], P, 0, 0, 0);
-}
-
 __device__ __forceinline__ f32x16 wy_load_vb(const MatBuf& M, int kw, int nb, int r0, int h, int l32, bool ok) {
   const int row = r0 + l32;
-  const int rr = row - kw;
   f32x16 vb;
+  if (r0 >= kw + nb && nb == 32) {
+    const bool okr = ok && row < M.n;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int refl = 8 * (j >> 2) + 4 * h + (j & 3);
+      vb[j] = buf_load(M.r, okr ? M.off(row, kw + refl) : kOffNone);
+    }
+    return vb;
+  }
+  const int rr = row - kw;
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
     const int refl = 8 * (j >> 2) + 4 * h + (j & 3);
@@ -151,9 +127,29 @@ __device__ __forceinline__ f32x16 wy_load_vb(const MatBuf& M, int kw, int nb, in
   return vb;
 }
 
+__device__ __forceinline__ void wy_mfma_p(f32x16& P, const f32x16& va, const f32x16& X) {
+#pragma unroll
+  for (int j = 0; j < 16; ++j) P = __builtin_amdgcn_mfma_f32_32x32x2f32(va[j], X[j], P, 0, 0, 0);
+}
+
 __device__ __forceinline__ void wy_mfma_apply(f32x16& X, const f32x16& vb, const f32x16& W) {
 #pragma unroll
   for (int j = 0; j < 16; ++j) X = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[j], W[j], X, 0, 0, 0);
+}
+
+// P += V^T X for one 32-row tile at r0.
+template <bool VEC>
+__device__ __forceinline__ void wy_accumulate(f32x16& P, const f32x16& X, const MatBuf& M, int kw, int nb, int r0,
+                                              int h, int l32) {
+  const f32x16 va = wy_load_va<VEC>(M, kw, nb, r0, h, l32, true);
+  wy_mfma_p(P, va, X);
+}
+
+// X += V W for one tile.
+__device__ __forceinline__ void wy_apply(f32x16& X, const f32x16& W, const MatBuf& M, int kw, int nb, int r0, int h,
+                                         int l32) {
+  const f32x16 vb = wy_load_vb(M, kw, nb, r0, h, l32, true);
+  wy_mfma_apply(X, vb, W);
 }
 
 }  // namespace fastqr
