@@ -159,7 +159,7 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
     // variants (short strips, many workgroups) gain more from the occupancy
     // the registers would cost, and 16 waves (128 registers each) leave no
     // room for it.
-    constexpr int PFM = (RES && TPW > 1 && NW == 8) ? 2 : 0;
+    constexpr int PFM = (RES && TPW > 1 && TPW <= 4 && NW == 8) ? 2 : 0;
     f32x16 vb[PFM == 2 ? TPW : 1];
     if constexpr (RES && PFM == 0) {
 #pragma unroll
@@ -286,19 +286,23 @@ hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, c
   // batches, narrow updates), and 4 per wave once the launch alone holds
   // about four waves per SIMD of the GPU.
   constexpr int64_t kWaveBudget = 4096;
+  // 16 waves (128 registers each) hold at most 2 tiles per wave without
+  // spilling; taller strips use 8 waves of up to 8 tiles.
   int nw = 0, tpw = 0;
   for (int t = 1; t <= 4; t *= 2) {
     int w = 1;
     while (w * t < ntiles) w *= 2;
-    if (w <= 16 && strips * batch * w <= kWaveBudget) {
+    if (w <= (t <= 2 ? 16 : 8) && strips * batch * w <= kWaveBudget) {
       nw = w, tpw = t;
       break;
     }
   }
-  if (nw == 0) {
+  if (nw == 0 && ntiles <= 32) {
     tpw = 4;
     nw = 1;
-    while (nw * 4 < ntiles && nw < 16) nw *= 2;
+    while (nw * 4 < ntiles) nw *= 2;
+  } else if (nw == 0) {
+    nw = 8, tpw = 8;
   }
   const bool res = nw * tpw >= ntiles;
   const int prio = hi_prio ? 1 : 0;
@@ -326,7 +330,7 @@ hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, c
   FASTQR_WY(2, 4, true)
   FASTQR_WY(4, 4, true)
   FASTQR_WY(8, 4, true)
-  FASTQR_WY(16, 4, true)
+  FASTQR_WY(8, 8, true)
 #undef FASTQR_WY
   // strips taller than 16 waves x 4 tiles: stream the tiles
   if (vec)
