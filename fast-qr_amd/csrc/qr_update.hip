@@ -57,6 +57,9 @@ __device__ __forceinline__ int64_t pp_index(int64_t b, int s, int rb, int blk, i
   return (((b * nstrips + s) * nrb + rb) * kWyrMaxBlk + blk) * 1024;
 }
 
+// Tiles of a row block are software-pipelined: the X and V loads of tile t+1
+// are issued before the MFMAs of tile t (loads past the block read zeros
+// through the buffer range check).
 template <int NBLK, bool VEC>
 __global__ void __launch_bounds__(64) wyr_partial_kernel(const float* __restrict__ H, int64_t hs0, int ldh, int n,
                                                          int kv, int k, int c_begin, int c_end, int gram_end,
@@ -67,10 +70,29 @@ __global__ void __launch_bounds__(64) wyr_partial_kernel(const float* __restrict
   const int lane = threadIdx.x, h = lane >> 5, l32 = lane & 31;
   const int col = c_begin + 32 * s + l32;
   const bool colok = col < c_end;
-  const bool is_v = col < gram_end;
+  const bool is_v = c_begin + 32 * s < gram_end;  // strip of the group's own columns: read as V
   const MatBuf M{make_rsrc(H + b * hs0, (uint32_t)(4 * ldh * n)), ldh, n};
   const int r_lo = kv + rb * rows_per_blk;
   const int r_hi = min(n, r_lo + rows_per_blk);
+
+  auto load_x = [&](int r0) -> f32x16 {
+    f32x16 x = tile_load<VEC>(M, r0, col, colok && r0 < r_hi, h);
+    if (is_v) {
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int row = r0 + acc_row(j, h);
+        x[j] = row < col ? 0.0f : (row == col ? 1.0f : x[j]);
+      }
+    }
+    return x;
+  };
+  auto load_v = [&](int r0, f32x16 (&v)[NBLK]) {
+#pragma unroll
+    for (int blk = 0; blk < NBLK; ++blk) {
+      const int kw = kv + 32 * blk;
+      v[blk] = wy_load_va<VEC>(M, kw, min(32, k - 32 * blk), r0, h, l32, r0 < r_hi && r0 + 32 > kw);
+    }
+  };
 
   f32x16 P[NBLK];
 #pragma unroll
@@ -78,21 +100,19 @@ __global__ void __launch_bounds__(64) wyr_partial_kernel(const float* __restrict
 #pragma unroll
     for (int j = 0; j < 16; ++j) P[blk][j] = 0.0f;
 
+  f32x16 X = load_x(r_lo);
+  f32x16 V[NBLK];
+  load_v(r_lo, V);
   for (int r0 = r_lo; r0 < r_hi; r0 += 32) {
-    f32x16 X = tile_load<VEC>(M, r0, col, colok, h);
-    if (is_v) {
+    const f32x16 Xn = load_x(r0 + 32);
+    f32x16 Vn[NBLK];
+    load_v(r0 + 32, Vn);
 #pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int row = r0 + acc_row(j, h);
-        X[j] = row < col ? 0.0f : (row == col ? 1.0f : X[j]);
-      }
-    }
+    for (int blk = 0; blk < NBLK; ++blk)
+      if (r0 + 32 > kv + 32 * blk) wy_mfma_p(P[blk], V[blk], X);
+    X = Xn;
 #pragma unroll
-    for (int blk = 0; blk < NBLK; ++blk) {
-      const int kw = kv + 32 * blk;
-      const int nbv = min(32, k - 32 * blk);
-      if (r0 + 32 > kw) wy_accumulate<VEC>(P[blk], X, M, kw, nbv, r0, h, l32);
-    }
+    for (int blk = 0; blk < NBLK; ++blk) V[blk] = Vn[blk];
   }
 #pragma unroll
   for (int blk = 0; blk < NBLK; ++blk) store_acc(Ppart + pp_index(b, s, rb, blk, nstrips, nrb), P[blk], lane);
@@ -236,15 +256,28 @@ __global__ void __launch_bounds__(64) wyr_apply_kernel(float* __restrict__ H, in
   f32x16 W[NBLK];
 #pragma unroll
   for (int blk = 0; blk < NBLK; ++blk) W[blk] = load_acc(Wbuf + ((b * nstrips_w + s) * kWyrMaxBlk + blk) * 1024, lane);
-  for (int r0 = r_lo; r0 < r_hi; r0 += 32) {
-    f32x16 X = tile_load<VEC>(M, r0, col, colok, h);
+
+  auto load_v = [&](int r0, f32x16 (&v)[NBLK]) {
 #pragma unroll
     for (int blk = 0; blk < NBLK; ++blk) {
       const int kw = kv + 32 * blk;
-      const int nbv = min(32, k - 32 * blk);
-      if (r0 + 32 > kw) wy_apply(X, W[blk], M, kw, nbv, r0, h, l32);
+      v[blk] = wy_load_vb(M, kw, min(32, k - 32 * blk), r0, h, l32, r0 < r_hi && r0 + 32 > kw);
     }
+  };
+  f32x16 X = tile_load<VEC>(M, r_lo, col, colok, h);
+  f32x16 V[NBLK];
+  load_v(r_lo, V);
+  for (int r0 = r_lo; r0 < r_hi; r0 += 32) {
+    const f32x16 Xn = tile_load<VEC>(M, r0 + 32, col, colok && r0 + 32 < r_hi, h);
+    f32x16 Vn[NBLK];
+    load_v(r0 + 32, Vn);
+#pragma unroll
+    for (int blk = 0; blk < NBLK; ++blk)
+      if (r0 + 32 > kv + 32 * blk) wy_mfma_apply(X, V[blk], W[blk]);
     tile_store<VEC>(M, r0, col, colok, h, X);
+    X = Xn;
+#pragma unroll
+    for (int blk = 0; blk < NBLK; ++blk) V[blk] = Vn[blk];
   }
 }
 
