@@ -19,7 +19,7 @@
 //   wyr_tg_kernel       one workgroup per matrix: sums the Gram partials and
 //                       joins the panels' T factors into the group T
 //                       (T_[1:j] = [[T_[1:j-1], -T_[1:j-1] G_[1:j-1,j] T_j], [0, T_j]]).
-//   wyr_w_kernel        one wave per strip: W = -T^T sum_rb P_rb.
+//   wyr_w_kernel        four waves per strip: W = -T^T sum_rb P_rb.
 //   wyr_apply_kernel    grid (strips, row blocks, batch), one wave: X_rb += V_rb W.
 //
 // Partial products are summed in a fixed order (no atomics), so results are
@@ -118,26 +118,49 @@ __global__ void __launch_bounds__(64) wyr_partial_kernel(const float* __restrict
   for (int blk = 0; blk < NBLK; ++blk) store_acc(Ppart + pp_index(b, s, rb, blk, nstrips, nrb), P[blk], lane);
 }
 
-// Sum the row-block partials of strips [0, gridDim.x) into Gsum (the Gram
-// matrix V^T V of the group's own strips): one wave per (strip, block, matrix).
-__global__ void __launch_bounds__(64) wyr_reduce_kernel(const float* __restrict__ Ppart, int nstrips, int nrb,
-                                                        float* __restrict__ Gsum) {
-  const int s = blockIdx.x, blk = blockIdx.y;
-  const int64_t b = blockIdx.z;
-  const int lane = threadIdx.x;
+// Sum of the row-block partials of one (strip, reflector block) by the four
+// waves of a workgroup: wave w adds row blocks w, w + 4, ... with independent
+// loads in flight, the four sums meet in LDS.  The order of additions is fixed
+// (bitwise reproducible).  Returns the total in wave 0's registers.
+constexpr int kSumWaves = 4;
+
+__device__ __forceinline__ f32x16 wave_partial_sum(const float* __restrict__ Ppart, int64_t b, int s, int blk,
+                                                   int nstrips, int nrb, int wave, int lane) {
   f32x16 acc;
 #pragma unroll
   for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
-  int rb = 0;
-  for (; rb + 4 <= nrb; rb += 4) {
+  int rb = wave;
+  for (; rb + 3 * kSumWaves < nrb; rb += 4 * kSumWaves) {
     f32x16 v[4];
 #pragma unroll
-    for (int u = 0; u < 4; ++u) v[u] = load_acc(Ppart + pp_index(b, s, rb + u, blk, nstrips, nrb), lane);
+    for (int u = 0; u < 4; ++u) v[u] = load_acc(Ppart + pp_index(b, s, rb + u * kSumWaves, blk, nstrips, nrb), lane);
 #pragma unroll
     for (int u = 0; u < 4; ++u) acc += v[u];
   }
-  for (; rb < nrb; ++rb) acc += load_acc(Ppart + pp_index(b, s, rb, blk, nstrips, nrb), lane);
-  store_acc(Gsum + ((b * kWyrMaxBlk + blk) * kWyrMaxBlk + s) * 1024, acc, lane);
+  for (; rb < nrb; rb += kSumWaves) acc += load_acc(Ppart + pp_index(b, s, rb, blk, nstrips, nrb), lane);
+  return acc;
+}
+
+// Sum the row-block partials of strips [0, gridDim.x) into Gsum (the Gram
+// matrix V^T V of the group's own strips): one workgroup per (strip, block,
+// matrix).
+__global__ void __launch_bounds__(kSumWaves * 64) wyr_reduce_kernel(const float* __restrict__ Ppart, int nstrips,
+                                                                    int nrb, float* __restrict__ Gsum) {
+  const int s = blockIdx.x, blk = blockIdx.y;
+  const int64_t b = blockIdx.z;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  __shared__ float red[kSumWaves][16][64];
+  const f32x16 acc = wave_partial_sum(Ppart, b, s, blk, nstrips, nrb, wave, lane);
+#pragma unroll
+  for (int j = 0; j < 16; ++j) red[wave][j][lane] = acc[j];
+  __syncthreads();
+  if (wave == 0) {
+    f32x16 tot;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) tot[j] = (red[0][j][lane] + red[1][j][lane]) + (red[2][j][lane] + red[3][j][lane]);
+    store_acc(Gsum + ((b * kWyrMaxBlk + blk) * kWyrMaxBlk + s) * 1024, tot, lane);
+  }
 }
 
 // Group T (k x k, leading dimension kWyrTgLd) from the Gram matrix (Gsum) and
@@ -195,50 +218,51 @@ __global__ void __launch_bounds__(1024) wyr_tg_kernel(const float* __restrict__ 
 }
 
 // W = -T^T sum_rb P_rb for the strips [s0, s0 + gridDim.x) of Ppart; T is the
-// k x k matrix at Tsrc (+ b * t_stride, leading dimension ldt).
+// k x k matrix at Tsrc (+ b * t_stride, leading dimension ldt).  Four waves:
+// the row-block sums of every reflector block are split over the waves and
+// combined in LDS; wave w then forms W block w (T upper triangular:
+// W_w = sum_{p <= w} T(p, w)^T P_p), its T values loaded before its MFMAs.
 template <int NBLK>
-__global__ void __launch_bounds__(64) wyr_w_kernel(const float* __restrict__ Ppart, int nstrips, int nrb, int s0,
-                                                   const float* __restrict__ Tsrc, int64_t t_stride, int ldt, int k,
-                                                   float* __restrict__ Wbuf, int nstrips_w) {
+__global__ void __launch_bounds__(kSumWaves * 64) wyr_w_kernel(const float* __restrict__ Ppart, int nstrips, int nrb,
+                                                               int s0, const float* __restrict__ Tsrc,
+                                                               int64_t t_stride, int ldt, int k,
+                                                               float* __restrict__ Wbuf, int nstrips_w) {
   const int s = blockIdx.x;
   const int64_t b = blockIdx.y;
-  const int lane = threadIdx.x, h = lane >> 5, l32 = lane & 31;
-  f32x16 P[NBLK];
+  const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  __shared__ float red[kSumWaves][NBLK][16][64];
 #pragma unroll
   for (int blk = 0; blk < NBLK; ++blk) {
+    const f32x16 acc = wave_partial_sum(Ppart, b, s0 + s, blk, nstrips, nrb, wave, lane);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) P[blk][j] = 0.0f;
-    int rb = 0;
-    for (; rb + 4 <= nrb; rb += 4) {
-      f32x16 v[4];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) v[u] = load_acc(Ppart + pp_index(b, s0 + s, rb + u, blk, nstrips, nrb), lane);
-#pragma unroll
-      for (int u = 0; u < 4; ++u) P[blk] += v[u];
-    }
-    for (; rb < nrb; ++rb) P[blk] += load_acc(Ppart + pp_index(b, s0 + s, rb, blk, nstrips, nrb), lane);
+    for (int j = 0; j < 16; ++j) red[wave][blk][j][lane] = acc[j];
   }
+  __syncthreads();
+  if (wave >= NBLK) return;
+  const int blk = wave;
   const float* Tb = Tsrc + b * t_stride;
+  f32x16 W;
 #pragma unroll
-  for (int blk = 0; blk < NBLK; ++blk) {
-    f32x16 W;
+  for (int j = 0; j < 16; ++j) W[j] = 0.0f;
 #pragma unroll
-    for (int j = 0; j < 16; ++j) W[j] = 0.0f;
-    // W_blk = sum_{blk' <= blk} T(blk', blk)^T P_blk'
+  for (int bp = 0; bp < NBLK; ++bp) {
+    if (bp > blk) break;
+    float t[16];
+    f32x16 P;
 #pragma unroll
-    for (int bp = 0; bp <= blk; ++bp) {
-#pragma unroll
-      for (int j = 0; j < 16; ++j) {
-        const int kk = 32 * bp + acc_row(j, h);
-        const int cc = 32 * blk + l32;
-        const float t = (kk < k && cc < k) ? Tb[kk * ldt + cc] : 0.0f;
-        W = __builtin_amdgcn_mfma_f32_32x32x2f32(t, P[bp][j], W, 0, 0, 0);
-      }
+    for (int j = 0; j < 16; ++j) {
+      const int kk = 32 * bp + acc_row(j, h);
+      const int cc = 32 * blk + l32;
+      t[j] = (kk < k && cc < k) ? Tb[kk * ldt + cc] : 0.0f;
+      P[j] = (red[0][bp][j][lane] + red[1][bp][j][lane]) + (red[2][bp][j][lane] + red[3][bp][j][lane]);
     }
 #pragma unroll
-    for (int j = 0; j < 16; ++j) W[j] = -W[j];
-    store_acc(Wbuf + ((b * nstrips_w + s) * kWyrMaxBlk + blk) * 1024, W, lane);
+    for (int j = 0; j < 16; ++j) W = __builtin_amdgcn_mfma_f32_32x32x2f32(t[j], P[j], W, 0, 0, 0);
   }
+#pragma unroll
+  for (int j = 0; j < 16; ++j) W[j] = -W[j];
+  store_acc(Wbuf + ((b * nstrips_w + s) * kWyrMaxBlk + blk) * 1024, W, lane);
 }
 
 template <int NBLK, bool VEC>
@@ -338,7 +362,8 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
   if (c.gram) {
     // Gram strips: sum the partials, then join the panels' T factors
     float* Gsum = Wbuf + (size_t)c.batch * nstrips * kWyrMaxBlk * 1024;
-    hipLaunchKernelGGL(wyr_reduce_kernel, dim3((unsigned)gram_strips, (unsigned)nblk, (unsigned)c.batch), dim3(64), 0,
+    hipLaunchKernelGGL(wyr_reduce_kernel, dim3((unsigned)gram_strips, (unsigned)nblk, (unsigned)c.batch),
+                       dim3(kSumWaves * 64), 0,
                        stream, Ppart, nstrips, nrb, Gsum);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(wyr_tg_kernel, dim3((unsigned)c.batch), dim3(1024), 0, stream, Gsum, c.Tws, c.slot0, c.q, c.nb,
@@ -355,19 +380,19 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
   const dim3 gw((unsigned)nx, (unsigned)c.batch);
   switch (nblk) {
     case 1:
-      hipLaunchKernelGGL((wyr_w_kernel<1>), gw, dim3(64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
+      hipLaunchKernelGGL((wyr_w_kernel<1>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
                          ldt, c.k, Wbuf, nx);
       break;
     case 2:
-      hipLaunchKernelGGL((wyr_w_kernel<2>), gw, dim3(64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
+      hipLaunchKernelGGL((wyr_w_kernel<2>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
                          ldt, c.k, Wbuf, nx);
       break;
     case 3:
-      hipLaunchKernelGGL((wyr_w_kernel<3>), gw, dim3(64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
+      hipLaunchKernelGGL((wyr_w_kernel<3>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
                          ldt, c.k, Wbuf, nx);
       break;
     default:
-      hipLaunchKernelGGL((wyr_w_kernel<4>), gw, dim3(64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
+      hipLaunchKernelGGL((wyr_w_kernel<4>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
                          ldt, c.k, Wbuf, nx);
       break;
   }
