@@ -381,39 +381,41 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   }
   if (use_rowsplit(batch, n)) return run_rowsplit(H, batch, h_s0, h_s2, tau, tau_s0, tau_s1, Tws, ni, vec, stream);
 
-  // Panels are processed in groups of up to kMaxWY.  Within a group each
-  // panel is followed by a narrow update of the group's remaining columns;
-  // the group's transforms are then applied together to the columns right of
-  // it.  Look-ahead: that wide update is split into the next group's columns
-  // (first) and the rest; the next group's panels run on a side stream while
-  // the rest is updated on the caller's stream.  T slots alternate between
-  // two banks by group parity.
+  // Panels are processed in groups of up to 128 columns (kMaxWY transforms
+  // of 32 columns, one T slot each).  A group is two panels of 64 columns or
+  // four of 32 (panel_width_wide); each panel but the group's last is followed by a narrow update
+  // of the group's remaining columns.  The group's transforms are then applied
+  // together to the columns right of it.  Look-ahead: that wide update is
+  // split into the next group's columns (first) and the rest; the next
+  // group's panels run on a side stream while the rest is updated on the
+  // caller's stream.  T slots alternate between two banks by group parity.
   struct Group {
-    int g0, nb, g_end, npan, slot_base;
+    int g0, pw, g_end, slot_base;
   };
+  constexpr int kTw = 32;  // transform width of the strip-resident update
   std::vector<Group> groups;
   for (int g0 = 0, gi = 0; g0 < ni; ++gi) {
-    const int nb = fastqr::panel_width_for(ni - g0);
-    const int g_end = (g0 + fastqr::kMaxWY * nb < ni) ? g0 + fastqr::kMaxWY * nb : ni;
-    groups.push_back(Group{g0, nb, g_end, (g_end - g0 + nb - 1) / nb, (gi & 1) * fastqr::kMaxWY});
+    const int g_end = (g0 + fastqr::kMaxWY * kTw < ni) ? g0 + fastqr::kMaxWY * kTw : ni;
+    groups.push_back(Group{g0, fastqr::panel_width_wide(ni - g0, batch), g_end, (gi & 1) * fastqr::kMaxWY});
     g0 = g_end;
   }
   auto run_panels = [&](const Group& G, hipStream_t st) -> hipError_t {
-    for (int i = 0; i < G.npan; ++i) {
-      const int pk = G.g0 + i * G.nb;
+    for (int pk = G.g0; pk < G.g_end; pk += G.pw) {
       const double m = ni - pk;
-      const double wd = (m < G.nb) ? m : G.nb;
+      const int wi = (G.g_end - pk < G.pw) ? G.g_end - pk : G.pw;
+      const double wd = wi;
+      const int slot = G.slot_base + (pk - G.g0) / kTw;
       hipError_t err = timed(kPanel, bd * (2.0 * m * wd * wd - 2.0 * wd * wd * wd / 3.0), bd * 8.0 * m * wd, st, [&] {
-        return fastqr::launch_panel(H, batch, h_s0, h_s2, tau, tau_s0, tau_s1, Tws, ni, pk, G.nb, ni - pk,
-                                    G.slot_base + i, vec, st);
+        return fastqr::launch_panel(H, batch, h_s0, h_s2, tau, tau_s0, tau_s1, Tws, ni, pk, G.pw, ni - pk, slot, vec,
+                                    st);
       });
       if (err != hipSuccess) return err;
-      const int c0 = pk + (int)wd;
+      const int c0 = pk + wi;
       if (c0 < G.g_end) {
         const double c = G.g_end - c0;
         err = timed(kUpdate, bd * 4.0 * m * wd * c, bd * (8.0 * m * c + 4.0 * m * wd), st, [&] {
-          return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, pk, G.nb, G.slot_base + i, 1, c0, G.g_end,
-                                          vec, true, st);
+          return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, pk, kTw, slot, (wi + kTw - 1) / kTw, c0,
+                                          G.g_end, vec, true, st);
         });
         if (err != hipSuccess) return err;
       }
@@ -424,8 +426,8 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
     if (c_end <= c_begin) return hipSuccess;
     const double m = ni - G.g0, wg = G.g_end - G.g0, c = c_end - c_begin;
     return timed(kUpdate, bd * 4.0 * m * wg * c, bd * (8.0 * m * c + 4.0 * m * wg), st, [&] {
-      return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, G.g0, G.nb, G.slot_base, G.npan, c_begin,
-                                      c_end, vec, critical, st);
+      return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, G.g0, kTw, G.slot_base,
+                                      (G.g_end - G.g0 + kTw - 1) / kTw, c_begin, c_end, vec, critical, st);
     });
   };
 

@@ -22,9 +22,12 @@ hipError_t launch_copy_colmajor(const float* A, int64_t batch, int n, int64_t as
                                 float* H, int64_t hs0, int64_t ldh, hipStream_t stream);
 // Panel width (32, or 16 above 2048 rows) and the tallest panel supported (qr_panel.hip).
 int panel_width_for(int m);
+// Panel width of the strip-resident path (64 or 32; T slots of 32 columns).
+int panel_width_wide(int m, int64_t batch);
 int panel_max_rows();
 // Panel of width nb at column k0, template sized for m_cap >= n - k0 rows;
-// its T factor goes to workspace slot `slot`.
+// its T factors go to workspace slots `slot` .. (one 32 x 32 slot per 32
+// columns; a 16-column panel uses one slot).
 // Explicit (waves, tiles per wave) variant of launch_panel, for tuning.
 hipError_t launch_panel_cfg(int nw, int tpw, float* H, int64_t batch, int64_t hs0, int64_t ldh, float* tau,
                             int64_t ts0, int64_t ts1, float* Tws, int n, int k0, int nb, int slot, bool vec,

@@ -113,7 +113,7 @@ __device__ __forceinline__ void wave_sync_lds() {
 template <int NW, int TPW, int NBLK, bool VEC, class IO>
 __device__ __forceinline__ void panel_body(IO& io, int m, int tid) {
   static_assert(NW == 1 || NW % 2 == 0, "wave count");
-  static_assert(NBLK == 1 || NBLK == 2, "16- or 32-column panels");
+  static_assert(NBLK == 1 || NBLK == 2 || NBLK == 4 || NBLK == 8, "16-, 32-, 64- or 128-column panels");
   static_assert(NW * TPW >= NBLK, "the panel's diagonal tiles must exist");
   constexpr int NB = 16 * NBLK;
   const int w = m < NB ? m : NB;
@@ -125,12 +125,18 @@ __device__ __forceinline__ void panel_body(IO& io, int m, int tid) {
   constexpr int NWR = NW > 1 ? NW : 2;
   // red[parity][column][wave]: per-wave partials (sum, row j) of one column step
   __shared__ __attribute__((aligned(16))) float2 red[2][16][NWR];
-  __shared__ float Ts[NB][NB + 1];
+  // T of each 32-column slot (blocks 2p and 2p+1): [[T_2p, T_2p,2p+1], [0, T_2p+1]]
+  constexpr int NPAIR = NBLK > 1 ? NBLK / 2 : 1;
+  __shared__ float Ts[NPAIR][32][33];
   __shared__ float Gs[16][17];
   __shared__ float Mt[16][17];
-  constexpr int NW2 = NBLK == 2 ? NW : 1;
-  __shared__ f32x4 Pp[NW2][64];
+  // block updates: partial products of up to PCH later blocks are summed over
+  // the waves in one LDS round
+  constexpr int NW2 = NBLK > 1 ? NW : 1;
+  constexpr int PCH = NBLK > 4 ? 4 : (NBLK > 1 ? NBLK - 1 : 1);
+  __shared__ f32x4 Pp[NW2][PCH][64];
   __shared__ float Vt[NW2][16][17];
+  for (int idx = tid; idx < NPAIR * 32 * 33; idx += NW * 64) (&Ts[0][0][0])[idx] = 0.0f;
 
   f32x4 X[NBLK][TPW];
 #pragma unroll
@@ -259,11 +265,11 @@ __device__ __forceinline__ void panel_body(IO& io, int m, int tid) {
     if constexpr (NW == 1) {
       return v;
     } else {
-      Pp[wave][lane] = v;
+      Pp[wave][0][lane] = v;
       io.barrier();
       f32x4 s = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int wv = 0; wv < NW; ++wv) s += Pp[wv][lane];
+      for (int wv = 0; wv < NW; ++wv) s += Pp[wv][0][lane];
       io.barrier();
       return s;
     }
@@ -271,90 +277,133 @@ __device__ __forceinline__ void panel_body(IO& io, int m, int tid) {
 
   auto store_trow = [&](int blk, const float (&trow)[16]) {
     if (wave == 0 && kq == 0) {
+      const int o = 16 * (blk & 1);
 #pragma unroll
-      for (int jj = 0; jj < 16; ++jj) Ts[16 * blk + cn][16 * blk + jj] = trow[jj];
+      for (int jj = 0; jj < 16; ++jj) Ts[blk >> 1][o + cn][o + jj] = trow[jj];
     }
   };
 
-  {
-    float trow[16];
-    factor_block(std::integral_constant<int, 0>{}, trow);
-    store_trow(0, trow);
-  }
+  // Apply block B's transform to every later block (right-looking inside the
+  // panel): P_c = V_B^T X_c, W_c = -(T_B^T P_c), X_c += V_B W_c, with 16x16x4
+  // MFMAs on the registers; V_B is transposed through a per-wave LDS tile once
+  // per tile for all later blocks.
+  auto apply_block = [&](auto b_c) {
+    constexpr int B = decltype(b_c)::value;
+    constexpr int NL = NBLK - 1 - B;  // later blocks
+    constexpr int PO = B >> 1, OO = 16 * (B & 1);
+    io.barrier();  // T_B in LDS
+    f32x4 W[NL];
+    unroll_seq(
+        [&](auto c0_c) {
+          constexpr int C0 = decltype(c0_c)::value * PCH;  // first later block of this chunk
+          if constexpr (C0 < NL) {
+            constexpr int NC = (NL - C0) < PCH ? (NL - C0) : PCH;
+            f32x4 P[NC];
+#pragma unroll
+            for (int k = 0; k < NC; ++k) P[k] = f32x4{0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+            for (int t = 0; t < TPW; ++t)
+#pragma unroll
+              for (int j = 0; j < 4; ++j) {
+                const float v = vval(B, t, j);
+#pragma unroll
+                for (int k = 0; k < NC; ++k) P[k] = mfma16(v, X[B + 1 + C0 + k][t][j], P[k]);
+              }
+            if constexpr (NW > 1) {
+#pragma unroll
+              for (int k = 0; k < NC; ++k) Pp[wave][k][lane] = P[k];
+              io.barrier();
+#pragma unroll
+              for (int k = 0; k < NC; ++k) {
+                f32x4 sum = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+                for (int wv = 0; wv < NW; ++wv) sum += Pp[wv][k][lane];
+                P[k] = sum;
+              }
+              io.barrier();
+            }
+#pragma unroll
+            for (int k = 0; k < NC; ++k) {
+              f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+#pragma unroll
+              for (int j = 0; j < 4; ++j) acc = mfma16(Ts[PO][OO + 4 * kq + j][OO + cn], P[k][j], acc);
+              W[C0 + k] = -acc;
+            }
+          }
+        },
+        std::make_integer_sequence<int, (NL + PCH - 1) / PCH>{});
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+#pragma unroll
+      for (int i = 0; i < 4; ++i) Vt[wave][4 * kq + i][cn] = vval(B, t, i);
+      wave_sync_lds();
+      float vt[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) vt[j] = Vt[wave][cn][4 * kq + j];
+#pragma unroll
+      for (int k = 0; k < NL; ++k)
+#pragma unroll
+        for (int j = 0; j < 4; ++j) X[B + 1 + k][t] = mfma16(vt[j], W[k][j], X[B + 1 + k][t]);
+      wave_sync_lds();
+    }
+  };
 
-  if constexpr (NBLK == 2) {
-    if (w > 16) {
-      io.barrier();  // T0 in LDS
-      // P = V0^T X1 (16 x 16)
-      f32x4 P = {0.0f, 0.0f, 0.0f, 0.0f};
+  // Join the T factors of blocks B-1 and B (B odd) into their 32-column slot:
+  // T_{B-1,B} = -T_{B-1} G T_B with G = V_{B-1}^T V_B.
+  auto join_pair = [&](auto b_c) {
+    constexpr int B = decltype(b_c)::value;
+    constexpr int PO = B >> 1;
+    f32x4 G = {0.0f, 0.0f, 0.0f, 0.0f};
 #pragma unroll
-      for (int t = 0; t < TPW; ++t)
+    for (int t = 0; t < TPW; ++t)
 #pragma unroll
-        for (int j = 0; j < 4; ++j) P = mfma16(vval(0, t, j), X[1][t][j], P);
-      P = wave_allreduce(P);
-      // W = -(T0^T P)
-      f32x4 W = {0.0f, 0.0f, 0.0f, 0.0f};
+      for (int j = 0; j < 4; ++j) G = mfma16(vval(B - 1, t, j), vval(B, t, j), G);
+    G = wave_allreduce(G);
+    if (wave == 0) {
 #pragma unroll
-      for (int j = 0; j < 4; ++j) W = mfma16(Ts[4 * kq + j][cn], P[j], W);
-      W = -W;
-      // X1 += V0 W, V0 transposed through a per-wave LDS tile
+      for (int j = 0; j < 4; ++j) Gs[4 * kq + j][cn] = G[j];
+    }
+    io.barrier();  // Gs and T_B visible
+    if (wave == 0) {
+      const int i = lane >> 2, j0 = 4 * (lane & 3);
 #pragma unroll
-      for (int t = 0; t < TPW; ++t) {
+      for (int jj = 0; jj < 4; ++jj) {
+        float acc = 0.0f;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) Vt[wave][4 * kq + i][cn] = vval(0, t, i);
-        wave_sync_lds();
-#pragma unroll
-        for (int j = 0; j < 4; ++j) X[1][t] = mfma16(Vt[wave][cn][4 * kq + j], W[j], X[1][t]);
-        wave_sync_lds();
+        for (int k = 0; k < 16; ++k) acc = fmaf(Ts[PO][i][k], Gs[k][j0 + jj], acc);
+        Mt[i][j0 + jj] = acc;
       }
-      {
-        float trow[16];
-        factor_block(std::integral_constant<int, 1>{}, trow);
-        store_trow(1, trow);
-      }
-      // G = V0^T V1
-      f32x4 G = {0.0f, 0.0f, 0.0f, 0.0f};
+      wave_sync_lds();
 #pragma unroll
-      for (int t = 0; t < TPW; ++t)
+      for (int jj = 0; jj < 4; ++jj) {
+        float acc = 0.0f;
 #pragma unroll
-        for (int j = 0; j < 4; ++j) G = mfma16(vval(0, t, j), vval(1, t, j), G);
-      G = wave_allreduce(G);
-      if (wave == 0) {
-#pragma unroll
-        for (int j = 0; j < 4; ++j) Gs[4 * kq + j][cn] = G[j];
-      }
-      io.barrier();  // Gs and T1 visible
-      // T01 = -(T0 G) T1 by wave 0, 4 entries per lane
-      if (wave == 0) {
-        const int i = lane >> 2, j0 = 4 * (lane & 3);
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          float acc = 0.0f;
-#pragma unroll
-          for (int k = 0; k < 16; ++k) acc = fmaf(Ts[i][k], Gs[k][j0 + jj], acc);
-          Mt[i][j0 + jj] = acc;
-        }
-        wave_sync_lds();
-#pragma unroll
-        for (int jj = 0; jj < 4; ++jj) {
-          float acc = 0.0f;
-#pragma unroll
-          for (int k = 0; k < 16; ++k) acc = fmaf(Mt[i][k], Ts[16 + k][16 + j0 + jj], acc);
-          Ts[i][16 + j0 + jj] = -acc;
-        }
-      }
-      for (int idx = tid; idx < 16 * 16; idx += NW * 64) Ts[16 + (idx >> 4)][idx & 15] = 0.0f;
-    } else {
-      // a narrow last panel: the other quadrants of T are zero
-      for (int idx = tid; idx < 32 * 32; idx += NW * 64) {
-        const int r = idx >> 5, c = idx & 31;
-        if (r >= 16 || c >= 16) Ts[r][c] = 0.0f;
+        for (int k = 0; k < 16; ++k) acc = fmaf(Mt[i][k], Ts[PO][16 + k][16 + j0 + jj], acc);
+        Ts[PO][i][16 + j0 + jj] = -acc;
       }
     }
-  }
+  };
+
+  io.barrier();  // zeroed T slots visible before any block writes its T
+  unroll_seq(
+      [&](auto b_c) {
+        constexpr int B = decltype(b_c)::value;
+        if (16 * B >= w) return;
+        {
+          float trow[16];
+          factor_block(b_c, trow);
+          store_trow(B, trow);
+        }
+        if constexpr ((B & 1) == 1) join_pair(b_c);
+        if constexpr (B + 1 < NBLK) {
+          if (16 * (B + 1) < w) apply_block(b_c);
+        }
+      },
+      std::make_integer_sequence<int, NBLK>{});
   io.barrier();
 
-  // write the panel, T (32 x 32 slot, zero outside the NB x NB corner) and tau
+  // write the panel, T (one 32 x 32 slot per 32 columns; a 16-column panel
+  // fills the upper-left quarter of one slot) and tau
 #pragma unroll
   for (int blk = 0; blk < NBLK; ++blk) {
 #pragma unroll
@@ -369,9 +418,9 @@ __device__ __forceinline__ void panel_body(IO& io, int m, int tid) {
       }
     }
   }
-  for (int idx = tid; idx < 32 * 32; idx += NW * 64) {
-    const int r = idx >> 5, c = idx & 31;
-    io.store_T(r, c, (r < NB && c < NB) ? Ts[r][c] : 0.0f);
+  for (int idx = tid; idx < NPAIR * 32 * 32; idx += NW * 64) {
+    const int p = idx >> 10, r = (idx >> 5) & 31, c = idx & 31;
+    io.store_T(p, r, c, Ts[p][r][c]);
   }
   if (wave == 0 && kq == 0) {
 #pragma unroll

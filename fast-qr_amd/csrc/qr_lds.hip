@@ -50,7 +50,7 @@ struct LdsPanelIO {
   __device__ __forceinline__ void store1(int r, int c, bool ok, float v) const {
     if (ok) M[idx(r, c)] = v;
   }
-  __device__ __forceinline__ void store_T(int r, int c, float v) const { T[r][c] = v; }
+  __device__ __forceinline__ void store_T(int /*slot*/, int r, int c, float v) const { T[r][c] = v; }
   __device__ __forceinline__ void store_tau(int c, float v) const { tau[(int64_t)(k0 + c) * ts1] = v; }
   __device__ __forceinline__ void barrier() const {
     if constexpr (NWP == 1) {
