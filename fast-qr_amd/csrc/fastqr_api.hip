@@ -415,19 +415,29 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
         const double c = G.g_end - c0;
         err = timed(kUpdate, bd * 4.0 * m * wd * c, bd * (8.0 * m * c + 4.0 * m * wd), st, [&] {
           return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, pk, kTw, slot, (wi + kTw - 1) / kTw, c0,
-                                          G.g_end, vec, true, st);
+                                          G.g_end, vec, true, 0, st);
         });
         if (err != hipSuccess) return err;
       }
     }
     return hipSuccess;
   };
+  // The wide update that overlaps the next group's panels leaves one CU per
+  // matrix to them when the batch is smaller than the GPU: each panel
+  // workgroup needs most of a CU's registers and would otherwise wait for a
+  // CU to drain behind the update's workgroups.
+  int num_cus = 0, dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess ||
+      hipDeviceGetAttribute(&num_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+    num_cus = 0;
+  const int rest_cus = (num_cus > 0 && batch < num_cus / 2) ? num_cus - (int)batch : 0;
   auto run_update = [&](const Group& G, int c_begin, int c_end, bool critical, hipStream_t st) -> hipError_t {
     if (c_end <= c_begin) return hipSuccess;
     const double m = ni - G.g0, wg = G.g_end - G.g0, c = c_end - c_begin;
     return timed(kUpdate, bd * 4.0 * m * wg * c, bd * (8.0 * m * c + 4.0 * m * wg), st, [&] {
       return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, G.g0, kTw, G.slot_base,
-                                      (G.g_end - G.g0 + kTw - 1) / kTw, c_begin, c_end, vec, critical, st);
+                                      (G.g_end - G.g0 + kTw - 1) / kTw, c_begin, c_end, vec, critical,
+                                      critical ? 0 : rest_cus, st);
     });
   };
 

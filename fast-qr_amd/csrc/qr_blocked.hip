@@ -11,6 +11,8 @@
 //                     accumulator layout and reused directly as the B operand of
 //                     V^T A2 by permuting the contraction index (any order of
 //                     the row sum is valid), so no register shuffles are needed.
+#include <unordered_map>
+
 #include "device.hpp"
 #include "kernels.hpp"
 #include "wy.hpp"
@@ -96,21 +98,9 @@ __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __re
 // operand, the contraction index permuted to match the accumulator layout),
 // P summed over waves in LDS, W = -(T^T P), X += V W.
 template <int NW, int TPW, bool RES, bool VEC>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu((TPW >= 2 && NW == 8) || (TPW >= 4 && NW <= 4) ? 2 : 4, 8)))
-wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* __restrict__ Tws, int n, int k0,
-                 int nb, int slot0, int nwy, int c_begin, int c_end, int hi_prio, int nstrips, int batch) {
-  // updates on the critical path (the rest of a panel group, the next group's
-  // columns) win issue arbitration against the wide update they overlap
-  if (hi_prio) __builtin_amdgcn_s_setprio(2);
-  // XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs, so
-  // workgroup L runs on XCD L % 8.  All strips of a matrix are given to one
-  // XCD (matrices xcd, xcd + 8, ... in turn), so the matrix's reflectors V,
-  // which every strip reads, are fetched into that XCD's L2 once.
-  const int L = blockIdx.x;
-  const int xk = L >> 3;
-  const int64_t b = (L & 7) + 8 * (xk / nstrips);
-  const int strip = xk % nstrips;
-  if (b >= batch) return;
+__device__ __forceinline__ void wy_update_item(float* __restrict__ H, int64_t hs0, int64_t ldh,
+                                               const float* __restrict__ Tws, int n, int k0, int nb, int slot0,
+                                               int nwy, int c_begin, int c_end, int64_t b, int strip) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar branches on tiles
   const int h = lane >> 5;
@@ -122,8 +112,17 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
   const MatBuf M{make_rsrc(H + b * hs0, (uint32_t)(4 * ldh * n)), (int)ldh, n};
 
   __shared__ float Ts[kMaxWY][32][33];
-  __shared__ float Pp[NW > 1 ? NW : 1][16][64];
   __shared__ float Pt[16][64];
+  // Per-wave LDS region: the wave's P partial (16 x 64) during the reduction
+  // over waves, then (up to 8 waves) the transpose tile through which the
+  // apply phase gets V from its pattern A registers.  A wave writes its
+  // region only after the barrier that ends every wave's reads of the
+  // partials, so the two uses never overlap.
+  constexpr bool LT = RES && NW <= 8;
+  constexpr int REG = LT ? 32 * 36 : 16 * 64;
+  __shared__ __attribute__((aligned(16))) float Wreg[NW > 1 || LT ? NW : 1][REG];
+  auto Pp = [&](int wv, int j) -> float* { return &Wreg[wv][j * 64]; };
+  auto VTs = [&](int wv) { return reinterpret_cast<float (*)[36]>(&Wreg[wv][0]); };
 
   for (int idx = threadIdx.x; idx < nwy * 32 * 32; idx += NW * 64) {
     const int i = idx >> 10, r = (idx >> 5) & 31, cc = idx & 31;
@@ -152,9 +151,9 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
 #pragma unroll
     for (int j = 0; j < 16; ++j) P[j] = 0.0f;
     // V prefetch depth: 0 = each tile's V loads next to its MFMAs, 2 = the V
-    // of all of this wave's tiles in flight at once (pattern A before the
-    // P MFMAs, pattern B before the reduction of P over the waves), at the
-    // cost of TPW more tiles of registers.  Measured on MI355X: it pays with
+    // of all of this wave's tiles in flight at once, loaded before the P
+    // MFMAs and kept (vb) for the apply phase, at the cost of TPW more tiles
+    // of registers.  Measured on MI355X: it pays with
     // 8 waves per workgroup (tall strips, few workgroups per CU); the 4-wave
     // variants (short strips, many workgroups) gain more from the occupancy
     // the registers would cost, and 16 waves (128 registers each) leave no
@@ -169,21 +168,15 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
         __builtin_amdgcn_sched_barrier(0);
       }
     } else if constexpr (RES) {
-      f32x16 va[TPW];
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const int rt = wave + NW * t;
-        va[t] = wy_load_va<VEC>(M, kw, nb, kb + 32 * rt, h, l32, rt < ntiles && rt >= rt_first);
+        vb[t] = wy_load_va<VEC>(M, kw, nb, kb + 32 * rt, h, l32, rt < ntiles && rt >= rt_first);
       }
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const int rt = wave + NW * t;
-        if (rt < ntiles && rt >= rt_first) wy_mfma_p(P, va[t], X[t]);
-      }
-#pragma unroll
-      for (int t = 0; t < TPW; ++t) {
-        const int rt = wave + NW * t;
-        vb[t] = wy_load_vb(M, kw, nb, kb + 32 * rt, h, l32, rt < ntiles && rt >= rt_first);
+        if (rt < ntiles && rt >= rt_first) wy_mfma_p(P, vb[t], X[t]);
       }
     } else {
       for (int rt = wave; rt < ntiles; rt += NW) {
@@ -195,7 +188,7 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
     if constexpr (NW > 1) {
       // sum over waves: each wave reduces 16/NW of the registers
 #pragma unroll
-      for (int j = 0; j < 16; ++j) Pp[wave][j][lane] = P[j];
+      for (int j = 0; j < 16; ++j) Pp(wave, j)[lane] = P[j];
       __syncthreads();
       constexpr int SL = 16 / NW;
 #pragma unroll
@@ -203,7 +196,7 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
         const int j = wave * SL + jj;
         float acc = 0.0f;
 #pragma unroll
-        for (int wv = 0; wv < NW; ++wv) acc += Pp[wv][j][lane];
+        for (int wv = 0; wv < NW; ++wv) acc += Pp(wv, j)[lane];
         Pt[j][lane] = acc;
       }
       __syncthreads();
@@ -220,18 +213,28 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
     }
 #pragma unroll
     for (int j = 0; j < 16; ++j) W[j] = -W[j];
-    if constexpr (RES && PFM == 0) {
+    if constexpr (RES && PFM == 0 && !LT) {
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const int rt = wave + NW * t;
         if (rt < ntiles && rt >= rt_first) wy_apply(X[t], W, M, kw, nb, kb + 32 * rt, h, l32);
         __builtin_amdgcn_sched_barrier(0);
       }
+    } else if constexpr (RES && PFM == 0) {
+#pragma unroll
+      for (int t = 0; t < TPW; ++t) {
+        const int rt = wave + NW * t;
+        if (rt < ntiles && rt >= rt_first) {
+          const f32x16 va = wy_load_va<VEC>(M, kw, nb, kb + 32 * rt, h, l32, true);
+          wy_mfma_apply(X[t], wy_transpose_va(VTs(wave), va, h, l32), W);
+        }
+        __builtin_amdgcn_sched_barrier(0);
+      }
     } else if constexpr (RES) {
 #pragma unroll
       for (int t = 0; t < TPW; ++t) {
         const int rt = wave + NW * t;
-        if (rt < ntiles && rt >= rt_first) wy_mfma_apply(X[t], vb[t], W);
+        if (rt < ntiles && rt >= rt_first) wy_mfma_apply(X[t], wy_transpose_va(VTs(wave), vb[t], h, l32), W);
       }
     } else {
       for (int rt = wave; rt < ntiles; rt += NW) {
@@ -257,6 +260,32 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
   }
 }
 
+// One work item = one (matrix, 32-column strip).  Items are taken in an
+// XCD-aware order: workgroups are dispatched round-robin over the 8 XCDs, so
+// workgroup L runs on XCD L % 8, and item L goes to matrix (L % 8) + 8 k, so
+// all strips of a matrix land on one XCD and the matrix's reflectors V, which
+// every strip reads, are fetched into that XCD's L2 once.  A grid smaller
+// than the item count loops (stride a multiple of 8, so each workgroup stays
+// on its XCD's matrices): the caller uses it to leave CUs free for the
+// critical-path kernels on the other stream.
+template <int NW, int TPW, bool RES, bool VEC>
+__global__ void __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu((TPW >= 2 && NW == 8) || (TPW >= 4 && NW <= 4) ? 2 : 4, 8)))
+wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* __restrict__ Tws, int n, int k0,
+                 int nb, int slot0, int nwy, int c_begin, int c_end, int hi_prio, int nstrips, int batch) {
+  // updates on the critical path (the rest of a panel group, the next group's
+  // columns) win issue arbitration against the wide update they overlap
+  if (hi_prio) __builtin_amdgcn_s_setprio(2);
+  const int total = 8 * ((batch + 7) >> 3) * nstrips;
+  for (int L = blockIdx.x; L < total; L += gridDim.x) {
+    const int xk = L >> 3;
+    const int64_t b = (L & 7) + 8 * (xk / nstrips);
+    const int strip = xk % nstrips;
+    if (b < batch) wy_update_item<NW, TPW, RES, VEC>(H, hs0, ldh, Tws, n, k0, nb, slot0, nwy, c_begin, c_end, b, strip);
+    __syncthreads();  // the next item rewrites the LDS buffers
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Host-side launchers
 // ---------------------------------------------------------------------------
@@ -270,17 +299,43 @@ hipError_t launch_copy_colmajor(const float* A, int64_t batch, int n, int64_t as
   return hipGetLastError();
 }
 
+namespace {
+
+// Workgroups of `kernel` resident per CU (queried once per kernel and thread).
+template <class K>
+int wgs_per_cu(K kernel, int threads) {
+  thread_local std::unordered_map<const void*, int> cache;
+  const void* key = reinterpret_cast<const void*>(kernel);
+  auto it = cache.find(key);
+  if (it != cache.end()) return it->second;
+  int v = 0;
+  if (hipOccupancyMaxActiveBlocksPerMultiprocessor(&v, kernel, threads, 0) != hipSuccess || v < 1) v = 1;
+  cache.emplace(key, v);
+  return v;
+}
+
+}  // namespace
+
 hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n,
                             int k0, int nb, int slot0, int nwy, int c_begin, int c_end, bool vec, bool hi_prio,
-                            hipStream_t stream) {
+                            int max_cus, hipStream_t stream) {
   const int cols = c_end - c_begin;
   if (cols <= 0 || nwy <= 0) return hipSuccess;
   const int ntiles = (n - k0 + 31) / 32;
   const int64_t strips = (cols + 31) / 32;
   const int64_t groups8 = (batch + 7) / 8;
-  if (8 * groups8 * strips > 0x7fffffffLL) return hipErrorInvalidValue;
-  const dim3 grid((unsigned)(8 * groups8 * strips));
+  const int64_t items = 8 * groups8 * strips;
+  if (items > 0x7fffffffLL) return hipErrorInvalidValue;
   const int ns = (int)strips, nbatch = (int)batch;
+  // grid: every item, or at most max_cus CUs' worth of resident workgroups
+  auto grid_for = [&](auto kernel, int threads) -> dim3 {
+    int64_t g = items;
+    if (max_cus > 0) {
+      const int64_t cap = ((int64_t)max_cus * wgs_per_cu(kernel, threads)) & ~(int64_t)7;
+      if (cap >= 8 && cap < g) g = cap;
+    }
+    return dim3((unsigned)g);
+  };
   // Tiles per wave: as few as the launch's size allows, so that a strip's
   // MFMA work is spread over several SIMDs when there are few strips (small
   // batches, narrow updates), and 4 per wave once the launch alone holds
@@ -309,10 +364,10 @@ hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, c
 #define FASTQR_WY(NW, TPW, RES)                                                                                 \
   if (nw == NW && tpw == TPW && res == RES) {                                                                   \
     if (vec)                                                                                                    \
-      hipLaunchKernelGGL((wy_update_kernel<NW, TPW, RES, true>), grid, dim3(NW * 64), 0, stream, H, hs0, ldh,    \
+      hipLaunchKernelGGL((wy_update_kernel<NW, TPW, RES, true>), grid_for(wy_update_kernel<NW, TPW, RES, true>, NW * 64), dim3(NW * 64), 0, stream, H, hs0, ldh,    \
                          Tws, n, k0, nb, slot0, nwy, c_begin, c_end, prio, ns, nbatch);                                     \
     else                                                                                                        \
-      hipLaunchKernelGGL((wy_update_kernel<NW, TPW, RES, false>), grid, dim3(NW * 64), 0, stream, H, hs0, ldh,   \
+      hipLaunchKernelGGL((wy_update_kernel<NW, TPW, RES, false>), grid_for(wy_update_kernel<NW, TPW, RES, false>, NW * 64), dim3(NW * 64), 0, stream, H, hs0, ldh,   \
                          Tws, n, k0, nb, slot0, nwy, c_begin, c_end, prio, ns, nbatch);                                     \
     return hipGetLastError();                                                                                   \
   }
@@ -334,10 +389,10 @@ hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, c
 #undef FASTQR_WY
   // strips taller than 16 waves x 4 tiles: stream the tiles
   if (vec)
-    hipLaunchKernelGGL((wy_update_kernel<16, 1, false, true>), grid, dim3(16 * 64), 0, stream, H, hs0, ldh, Tws, n,
+    hipLaunchKernelGGL((wy_update_kernel<16, 1, false, true>), grid_for(wy_update_kernel<16, 1, false, true>, 1024), dim3(16 * 64), 0, stream, H, hs0, ldh, Tws, n,
                        k0, nb, slot0, nwy, c_begin, c_end, prio, ns, nbatch);
   else
-    hipLaunchKernelGGL((wy_update_kernel<16, 1, false, false>), grid, dim3(16 * 64), 0, stream, H, hs0, ldh, Tws, n,
+    hipLaunchKernelGGL((wy_update_kernel<16, 1, false, false>), grid_for(wy_update_kernel<16, 1, false, false>, 1024), dim3(16 * 64), 0, stream, H, hs0, ldh, Tws, n,
                        k0, nb, slot0, nwy, c_begin, c_end, prio, ns, nbatch);
   return hipGetLastError();
 }

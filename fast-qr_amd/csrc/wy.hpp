@@ -137,6 +137,22 @@ __device__ __forceinline__ void wy_mfma_apply(f32x16& X, const f32x16& vb, const
   for (int j = 0; j < 16; ++j) X = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[j], W[j], X, 0, 0, 0);
 }
 
+// Pattern B of a tile from its pattern A registers, transposed through a
+// per-wave LDS tile VT[32 reflectors][32 rows (+4 pad)]: the float4 writes
+// (8 lanes, 36-word stride) and the row-contiguous reads are conflict-free.
+// Replaces 16 strided global loads per lane by one LDS round trip.
+__device__ __forceinline__ f32x16 wy_transpose_va(float (*VT)[36], const f32x16& va, int h, int l32) {
+#pragma unroll
+  for (int q = 0; q < 4; ++q)
+    *reinterpret_cast<f32x4*>(&VT[l32][8 * q + 4 * h]) = f32x4{va[4 * q], va[4 * q + 1], va[4 * q + 2], va[4 * q + 3]};
+  wave_sync_lds();
+  f32x16 vb;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) vb[j] = VT[8 * (j >> 2) + 4 * h + (j & 3)][l32];
+  wave_sync_lds();
+  return vb;
+}
+
 // P += V^T X for one 32-row tile at r0.
 template <bool VEC>
 __device__ __forceinline__ void wy_accumulate(f32x16& P, const f32x16& X, const MatBuf& M, int kw, int nb, int r0,
