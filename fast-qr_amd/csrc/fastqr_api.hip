@@ -450,27 +450,39 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
     }
     return FASTQR_OK;
   }
+  // The panels and the look-ahead updates (the critical path) run in order on
+  // the side stream.  The wide update of each group's remaining columns runs
+  // on the caller's stream after the group's look-ahead update (not beside
+  // it: the look-ahead is on the critical path), overlapping the next
+  // group's panels.  The look-ahead of group g waits for the wide update of
+  // group g-1, which produced the columns it reads (and last read the T bank
+  // that group g+1's panels overwrite).
   const hipStream_t side = aux->side;
-  hipEvent_t ev = aux->take();
-  if (!ev) return fail(FASTQR_EINVAL, "cannot create HIP events");
-  // the side stream must not run ahead of work already queued on `stream`
-  if ((e = hipEventRecord(ev, stream)) != hipSuccess || (e = hipStreamWaitEvent(side, ev, 0)) != hipSuccess)
-    return hip_fail(e, "stream join");
-  e = run_panels(groups[0], stream);
-  if (e != hipSuccess) return hip_fail(e, "panel launch");
+  auto record = [&](hipStream_t st) -> hipEvent_t {
+    hipEvent_t evt = aux->take();
+    if (evt && hipEventRecord(evt, st) != hipSuccess) evt = nullptr;
+    return evt;
+  };
+  hipEvent_t ev = record(stream);  // the side stream must not run ahead of work already queued on `stream`
+  if (!ev) return fail(FASTQR_EINVAL, "cannot record HIP events");
+  if ((e = hipStreamWaitEvent(side, ev, 0)) != hipSuccess) return hip_fail(e, "stream join");
+  if ((e = run_panels(groups[0], side)) != hipSuccess) return hip_fail(e, "panel launch");
+  hipEvent_t ev_rest = nullptr;
   for (size_t g = 0; g + 1 < groups.size(); ++g) {
     const Group& G = groups[g];
     const Group& Nx = groups[g + 1];
-    hipEvent_t ev_next = aux->take(), ev_pan = aux->take();
-    if (!ev_next || !ev_pan) return fail(FASTQR_EINVAL, "cannot create HIP events");
-    if ((e = run_update(G, Nx.g0, Nx.g_end, true, stream)) != hipSuccess) return hip_fail(e, "update launch");
-    if ((e = hipEventRecord(ev_next, stream)) != hipSuccess || (e = hipStreamWaitEvent(side, ev_next, 0)) != hipSuccess)
-      return hip_fail(e, "stream join");
+    if (ev_rest && (e = hipStreamWaitEvent(side, ev_rest, 0)) != hipSuccess) return hip_fail(e, "stream join");
+    if ((e = run_update(G, Nx.g0, Nx.g_end, true, side)) != hipSuccess) return hip_fail(e, "update launch");
+    hipEvent_t ev_la = record(side);
+    if (!ev_la) return fail(FASTQR_EINVAL, "cannot record HIP events");
     if ((e = run_panels(Nx, side)) != hipSuccess) return hip_fail(e, "panel launch");
-    if ((e = hipEventRecord(ev_pan, side)) != hipSuccess) return hip_fail(e, "stream join");
+    if ((e = hipStreamWaitEvent(stream, ev_la, 0)) != hipSuccess) return hip_fail(e, "stream join");
     if ((e = run_update(G, Nx.g_end, ni, false, stream)) != hipSuccess) return hip_fail(e, "update launch");
-    if ((e = hipStreamWaitEvent(stream, ev_pan, 0)) != hipSuccess) return hip_fail(e, "stream join");
+    if (!(ev_rest = record(stream))) return fail(FASTQR_EINVAL, "cannot record HIP events");
   }
+  hipEvent_t ev_end = record(side);
+  if (!ev_end) return fail(FASTQR_EINVAL, "cannot record HIP events");
+  if ((e = hipStreamWaitEvent(stream, ev_end, 0)) != hipSuccess) return hip_fail(e, "stream join");
   return FASTQR_OK;
 }
 
