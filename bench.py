@@ -72,7 +72,7 @@ def parse_args():
 
 
 # ---- HBM traffic from rocprofv3 counters ---------------------------------------
-TRAFFIC_SUMMARY = "hbm_traffic_bench_all_workloads.md"
+TRAFFIC_SUMMARY = "hbm_traffic_bench_all_workloads.txt"
 CALIB_BYTES = 256 * 1024 * 1024
 KIND_OF = (("panel_kernel", "panel"), ("wy_update_kernel", "update"), ("wyr_", "update_rowsplit"),
            ("copy_to_colmajor", "copy"), ("qr_wave_kernel", "wave64"), ("qr_lds_kernel", "lds"))
@@ -127,7 +127,8 @@ def summarize_traffic(fetch_dir: str, write_dir: str) -> str:
         "--steps 1 --warmup 0 --no-profile --no-check --cpu-sample-seconds 0 --calibrate-copy",
         "cd /tmp && rocprofv3 --pmc WRITE_SIZE -d $REPO/gpurun_out/pmc_bwrite -o run -f csv -- python3 $REPO/bench.py "
         "--steps 1 --warmup 0 --no-profile --no-check --cpu-sample-seconds 0 --calibrate-copy",
-        "python3 bench.py --summarize-traffic gpurun_out/pmc_bfetch gpurun_out/pmc_bwrite",
+        "python3 bench.py --summarize-traffic gpurun_out/pmc_bfetch gpurun_out/pmc_bwrite "
+        "> profiles/hbm_traffic_bench_all_workloads.txt",
         "```",
         "",
         "Calibration: a plain 256 MiB device copy (`__amd_rocclr_copyBuffer`) in the same run; each counter is "
