@@ -229,6 +229,7 @@ int run_rowsplit(float* H, int64_t batch, int64_t hs0, int64_t ldh, float* tau, 
       if (pk + w < G.g_end) {
         WyrCall c = base_call(pk, w, pk + w, G.g_end, area[0]);
         c.Tslot = Tws + (G.slot_base + i) * 1024;
+        c.hi_prio = true;
         if ((e = run_wyr(c, side)) != hipSuccess) return hip_fail(e, "narrow update launch");
       }
     }
@@ -244,6 +245,7 @@ int run_rowsplit(float* H, int64_t batch, int64_t hs0, int64_t ldh, float* tau, 
     c.nb = G.nb;
     c.slot0 = G.slot_base;
     c.Tg = Tg;
+    c.hi_prio = true;
     if ((e = run_wyr(c, side)) != hipSuccess) return hip_fail(e, "look-ahead update launch");
     if (Nx.g_end < n) {
       if ((e = join(stream, side)) != hipSuccess) return hip_fail(e, "stream join");

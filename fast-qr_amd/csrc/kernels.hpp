@@ -67,6 +67,7 @@ struct WyrCall {
   float* scratch;       // partial products and W (wyr_workspace_floats(batch, n) floats)
   int rows_per_blk;     // multiple of 32
   bool vec;
+  bool hi_prio;         // critical path: the waves win issue arbitration on shared SIMDs
 };
 hipError_t launch_wyr(const WyrCall& c, hipStream_t stream);
 int wyr_rows_per_block(int m, int64_t batch, int cols);

@@ -64,7 +64,8 @@ template <int NBLK, bool VEC>
 __global__ void __launch_bounds__(64) wyr_partial_kernel(const float* __restrict__ H, int64_t hs0, int ldh, int n,
                                                          int kv, int k, int c_begin, int c_end, int gram_end,
                                                          int rows_per_blk, float* __restrict__ Ppart, int nstrips,
-                                                         int nrb) {
+                                                         int nrb, int hi) {
+  if (hi) __builtin_amdgcn_s_setprio(2);
   const int s = blockIdx.x, rb = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int lane = threadIdx.x, h = lane >> 5, l32 = lane & 31;
@@ -145,7 +146,8 @@ __device__ __forceinline__ f32x16 wave_partial_sum(const float* __restrict__ Ppa
 // matrix V^T V of the group's own strips): one workgroup per (strip, block,
 // matrix).
 __global__ void __launch_bounds__(kSumWaves * 64) wyr_reduce_kernel(const float* __restrict__ Ppart, int nstrips,
-                                                                    int nrb, float* __restrict__ Gsum) {
+                                                                    int nrb, float* __restrict__ Gsum, int hi) {
+  if (hi) __builtin_amdgcn_s_setprio(2);
   const int s = blockIdx.x, blk = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int lane = threadIdx.x & 63;
@@ -166,7 +168,9 @@ __global__ void __launch_bounds__(kSumWaves * 64) wyr_reduce_kernel(const float*
 // Group T (k x k, leading dimension kWyrTgLd) from the Gram matrix (Gsum) and
 // the panels' T factors (q panels of width nb in workspace slots slot0 ..).
 __global__ void __launch_bounds__(1024) wyr_tg_kernel(const float* __restrict__ Gsum, const float* __restrict__ Tws,
-                                                      int slot0, int q, int nb, int k, float* __restrict__ Tg) {
+                                                      int slot0, int q, int nb, int k, float* __restrict__ Tg,
+                                                      int hi) {
+  if (hi) __builtin_amdgcn_s_setprio(2);
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
   __shared__ float Gs[kWyrMaxK][kWyrMaxK + 1];
@@ -226,7 +230,8 @@ template <int NBLK>
 __global__ void __launch_bounds__(kSumWaves * 64) wyr_w_kernel(const float* __restrict__ Ppart, int nstrips, int nrb,
                                                                int s0, const float* __restrict__ Tsrc,
                                                                int64_t t_stride, int ldt, int k,
-                                                               float* __restrict__ Wbuf, int nstrips_w) {
+                                                               float* __restrict__ Wbuf, int nstrips_w, int hi) {
+  if (hi) __builtin_amdgcn_s_setprio(2);
   const int s = blockIdx.x;
   const int64_t b = blockIdx.y;
   const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
@@ -268,7 +273,8 @@ __global__ void __launch_bounds__(kSumWaves * 64) wyr_w_kernel(const float* __re
 template <int NBLK, bool VEC>
 __global__ void __launch_bounds__(64) wyr_apply_kernel(float* __restrict__ H, int64_t hs0, int ldh, int n, int kv,
                                                        int k, int c_begin, int c_end, int rows_per_blk,
-                                                       const float* __restrict__ Wbuf, int nstrips_w) {
+                                                       const float* __restrict__ Wbuf, int nstrips_w, int hi) {
+  if (hi) __builtin_amdgcn_s_setprio(2);
   const int s = blockIdx.x, rb = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int lane = threadIdx.x, h = lane >> 5, l32 = lane & 31;
@@ -334,6 +340,7 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
   const int nstrips = (c.c_end - c.c_begin + 31) / 32;
   const int gram_strips = c.gram ? nblk : 0;  // the first strips of [c_begin, c_end) are the group's own columns
   const int gram_end = c.gram ? c.kv + c.k : 0;
+  const int hi = c.hi_prio ? 1 : 0;
   float* Ppart = c.scratch;
   float* Wbuf = c.scratch + (size_t)c.batch * nstrips * nrb * kWyrMaxBlk * 1024;
   const dim3 gp((unsigned)nstrips, (unsigned)nrb, (unsigned)c.batch);
@@ -341,10 +348,10 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
   do {                                                                                                             \
     if (c.vec)                                                                                                     \
       hipLaunchKernelGGL((wyr_partial_kernel<NB_, true>), gp, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv,   \
-                         c.k, c.c_begin, c.c_end, gram_end, c.rows_per_blk, Ppart, nstrips, nrb);                   \
+                         c.k, c.c_begin, c.c_end, gram_end, c.rows_per_blk, Ppart, nstrips, nrb, hi);                   \
     else                                                                                                           \
       hipLaunchKernelGGL((wyr_partial_kernel<NB_, false>), gp, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv,  \
-                         c.k, c.c_begin, c.c_end, gram_end, c.rows_per_blk, Ppart, nstrips, nrb);                   \
+                         c.k, c.c_begin, c.c_end, gram_end, c.rows_per_blk, Ppart, nstrips, nrb, hi);                   \
   } while (0)
   switch (nblk) {
     case 1: WYR_PARTIAL(1); break;
@@ -364,10 +371,10 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
     float* Gsum = Wbuf + (size_t)c.batch * nstrips * kWyrMaxBlk * 1024;
     hipLaunchKernelGGL(wyr_reduce_kernel, dim3((unsigned)gram_strips, (unsigned)nblk, (unsigned)c.batch),
                        dim3(kSumWaves * 64), 0,
-                       stream, Ppart, nstrips, nrb, Gsum);
+                       stream, Ppart, nstrips, nrb, Gsum, hi);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(wyr_tg_kernel, dim3((unsigned)c.batch), dim3(1024), 0, stream, Gsum, c.Tws, c.slot0, c.q, c.nb,
-                       c.k, c.Tg);
+                       c.k, c.Tg, hi);
     if ((e = hipGetLastError()) != hipSuccess) return e;
   }
   if (c.use_tg) {
@@ -381,19 +388,19 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
   switch (nblk) {
     case 1:
       hipLaunchKernelGGL((wyr_w_kernel<1>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
-                         ldt, c.k, Wbuf, nx);
+                         ldt, c.k, Wbuf, nx, hi);
       break;
     case 2:
       hipLaunchKernelGGL((wyr_w_kernel<2>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
-                         ldt, c.k, Wbuf, nx);
+                         ldt, c.k, Wbuf, nx, hi);
       break;
     case 3:
       hipLaunchKernelGGL((wyr_w_kernel<3>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
-                         ldt, c.k, Wbuf, nx);
+                         ldt, c.k, Wbuf, nx, hi);
       break;
     default:
       hipLaunchKernelGGL((wyr_w_kernel<4>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
-                         ldt, c.k, Wbuf, nx);
+                         ldt, c.k, Wbuf, nx, hi);
       break;
   }
   if ((e = hipGetLastError()) != hipSuccess) return e;
@@ -403,10 +410,10 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
   do {                                                                                                             \
     if (c.vec)                                                                                                     \
       hipLaunchKernelGGL((wyr_apply_kernel<NB_, true>), ga, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv, c.k, \
-                         xc_begin, c.c_end, c.rows_per_blk, Wbuf, nx);                                             \
+                         xc_begin, c.c_end, c.rows_per_blk, Wbuf, nx, hi);                                             \
     else                                                                                                           \
       hipLaunchKernelGGL((wyr_apply_kernel<NB_, false>), ga, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv,    \
-                         c.k, xc_begin, c.c_end, c.rows_per_blk, Wbuf, nx);                                        \
+                         c.k, xc_begin, c.c_end, c.rows_per_blk, Wbuf, nx, hi);                                        \
   } while (0)
   switch (nblk) {
     case 1: WYR_APPLY(1); break;

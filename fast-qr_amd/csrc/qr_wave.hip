@@ -44,13 +44,20 @@ struct make_seq<0, I...> {
 template <int NT>
 struct WaveQR {
   f32x4 X[NT][NT];
-  float tv[NT];
+  float tv[NT];   // lane cn: tau of column 16 tc + cn
+  float inv[NT];  // lane cn: 1 / (alpha - beta) of column 16 tc + cn (applied after the last step)
   int kq, cn;
 
   // one Householder step on column J (compile-time), for n > J
   template <int J>
   __device__ __forceinline__ void step() {
     constexpr int TJ = J / 16, JJ = J % 16, KQJ = JJ / 4, IJ = JJ % 4;
+    // row J of every column: register IJ of tile row TJ in DPP row KQJ, zero
+    // in the other rows, so the cross-row sums that total the dot products
+    // also broadcast it to every lane
+    float rt[NT];
+#pragma unroll
+    for (int tc = TJ; tc < NT; ++tc) rt[tc] = (kq == KQJ) ? X[TJ][tc][IJ] : 0.0f;
     // pivot column, broadcast along each 16-lane row; rows <= J masked
     f32x4 xb[NT];
 #pragma unroll
@@ -61,7 +68,7 @@ struct WaveQR {
         xb[tr][i] = (tr > TJ || 4 * kq + i > JJ) ? v : 0.0f;
       }
     }
-    float g[NT], rt[NT];
+    float g[NT];
 #pragma unroll
     for (int tc = TJ; tc < NT; ++tc) {
       float a0 = 0.0f, a1 = 0.0f;
@@ -73,21 +80,14 @@ struct WaveQR {
         a1 = fmaf(xb[tr][3], X[tr][tc][3], a1);
       }
       g[tc] = a0 + a1;
-      rt[tc] = (kq == KQJ) ? X[TJ][tc][IJ] : 0.0f;
     }
 #pragma unroll
-    for (int tc = TJ; tc < NT; ++tc) {
-      g[tc] = xor16_sum(g[tc]);
-      rt[tc] = xor16_sum(rt[tc]);
-    }
+    for (int tc = TJ; tc < NT; ++tc) g[tc] = xor16_sum(g[tc]), rt[tc] = xor16_sum(rt[tc]);
 #pragma unroll
-    for (int tc = TJ; tc < NT; ++tc) {
-      g[tc] = xor32_sum(g[tc]);
-      rt[tc] = xor32_sum(rt[tc]);
-    }
-    // lane JJ (kq 0) holds column J's totals
-    const float sigma = readlane(g[TJ], JJ);
+    for (int tc = TJ; tc < NT; ++tc) g[tc] = xor32_sum(g[tc]), rt[tc] = xor32_sum(rt[tc]);
     const float alpha = readlane(rt[TJ], JJ);
+    // lane JJ holds column J's totals
+    const float sigma = readlane(g[TJ], JJ);
     const Reflector rf = make_reflector_sel(alpha, sigma);
     float alp[NT], s[NT];
 #pragma unroll
@@ -96,7 +96,9 @@ struct WaveQR {
       s[tc] = (tc > TJ || cn > JJ) ? rf.tau * z : 0.0f;
       alp[tc] = -s[tc] * rf.inv;
     }
-    // a_r[c] -= tau z_c v_r,  v_r = x_r * inv below row J (x is 0 at rows <= J)
+    // a_r[c] -= tau z_c v_r,  v_r = x_r * inv below row J (x is 0 at rows <= J);
+    // the pivot column (s = 0) keeps its unscaled x: v = x * inv is applied
+    // once after the last step
 #pragma unroll
     for (int tr = TJ; tr < NT; ++tr) {
 #pragma unroll
@@ -105,23 +107,27 @@ struct WaveQR {
         for (int i = 0; i < 4; ++i) X[tr][tc][i] = fmaf(alp[tc], xb[tr][i], X[tr][tc][i]);
       }
     }
+    // row J: a_J[c] - s_c for c > J, beta on the diagonal
     if (kq == KQJ) {
 #pragma unroll
-      for (int tc = TJ; tc < NT; ++tc) X[TJ][tc][IJ] -= s[tc];
+      for (int tc = TJ; tc < NT; ++tc)
+        X[TJ][tc][IJ] = (tc == TJ && cn == JJ) ? rf.beta : X[TJ][tc][IJ] - s[tc];
     }
-    // the pivot column: beta on the diagonal, v = x * inv below it
-    if (cn == JJ) {
+    tv[TJ] = (cn == JJ) ? rf.tau : tv[TJ];
+    inv[TJ] = (cn == JJ) ? rf.inv : inv[TJ];
+  }
+
+  // v = x * inv below the diagonal of every column
+  __device__ __forceinline__ void scale_reflectors() {
 #pragma unroll
-      for (int tr = TJ; tr < NT; ++tr) {
+    for (int tr = 0; tr < NT; ++tr)
+#pragma unroll
+      for (int tc = 0; tc <= tr; ++tc)
 #pragma unroll
         for (int i = 0; i < 4; ++i) {
-          const int r = 16 * tr + 4 * kq + i;
-          if (r > J) X[tr][TJ][i] *= rf.inv;
-          if (r == J) X[tr][TJ][i] = rf.beta;
+          const int r = 16 * tr + 4 * kq + i, c = 16 * tc + cn;
+          if (r > c) X[tr][tc][i] *= inv[tc];
         }
-      }
-      tv[TJ] = rf.tau;
-    }
   }
 
   template <int... J>
@@ -154,9 +160,11 @@ __global__ void __launch_bounds__(64) qr_wave_kernel(const float* __restrict__ A
       }
     }
     q.tv[tr] = 0.0f;
+    q.inv[tr] = 0.0f;
   }
 
   q.run(n, typename make_seq<16 * NT>::type{});
+  q.scale_reflectors();
 
   float* Hb = H + b * hs0;
   const bool vec = hs1 == 1 && (hs2 & 3) == 0 && (hs0 & 3) == 0 && ((uintptr_t)H & 15) == 0;
