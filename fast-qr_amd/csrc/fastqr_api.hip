@@ -375,13 +375,17 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   const bool vec = ((uintptr_t)H % 16 == 0) && (h_s0 % 4 == 0) && (h_s2 % 4 == 0) && (n % 4 == 0);
   hipError_t e = hipSuccess;
   const double bd = (double)batch;
-  if (!same) {
-    e = timed(kCopy, 0.0, bd * 8.0 * (double)n * (double)n, stream, [&] {
-      return fastqr::launch_copy_colmajor(A, batch, ni, a_s0, a_s1, a_s2, H, h_s0, h_s2, stream);
+  // A -> H, columns [c0, c1)
+  auto copy_cols = [&](int c0, int c1) -> hipError_t {
+    if (same || c1 <= c0) return hipSuccess;
+    return timed(kCopy, 0.0, bd * 8.0 * (double)n * (double)(c1 - c0), stream, [&] {
+      return fastqr::launch_copy_colmajor(A, batch, ni, a_s0, a_s1, a_s2, H, h_s0, h_s2, c0, c1, stream);
     });
-    if (e != hipSuccess) return hip_fail(e, "copy launch");
+  };
+  if (use_rowsplit(batch, n)) {
+    if ((e = copy_cols(0, ni)) != hipSuccess) return hip_fail(e, "copy launch");
+    return run_rowsplit(H, batch, h_s0, h_s2, tau, tau_s0, tau_s1, Tws, ni, vec, stream);
   }
-  if (use_rowsplit(batch, n)) return run_rowsplit(H, batch, h_s0, h_s2, tau, tau_s0, tau_s1, Tws, ni, vec, stream);
 
   // Panels are processed in groups of up to 128 columns (kMaxWY transforms
   // of 32 columns, one T slot each).  A group is two panels of 64 columns or
@@ -444,6 +448,12 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   };
 
   DeviceAux* aux = groups.size() > 2 ? device_aux() : nullptr;
+  // With the side stream, only the first group's columns are copied before
+  // its panels start; the rest of the copy (HBM-bound) runs on the caller's
+  // stream beside those panels (latency-bound) and ahead of the first
+  // look-ahead update, the first kernel that reads those columns.
+  const int c_first = aux ? groups[0].g_end : ni;
+  if ((e = copy_cols(0, c_first)) != hipSuccess) return hip_fail(e, "copy launch");
   if (!aux) {
     for (const Group& G : groups) {
       e = run_panels(G, stream);
@@ -469,7 +479,10 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   if (!ev) return fail(FASTQR_EINVAL, "cannot record HIP events");
   if ((e = hipStreamWaitEvent(side, ev, 0)) != hipSuccess) return hip_fail(e, "stream join");
   if ((e = run_panels(groups[0], side)) != hipSuccess) return hip_fail(e, "panel launch");
-  hipEvent_t ev_rest = nullptr;
+  if ((e = copy_cols(c_first, ni)) != hipSuccess) return hip_fail(e, "copy launch");
+  // the first look-ahead waits for the copy (then for each wide update)
+  hipEvent_t ev_rest = c_first < ni ? record(stream) : nullptr;
+  if (c_first < ni && !ev_rest) return fail(FASTQR_EINVAL, "cannot record HIP events");
   for (size_t g = 0; g + 1 < groups.size(); ++g) {
     const Group& G = groups[g];
     const Group& Nx = groups[g + 1];

@@ -18,8 +18,10 @@ hipError_t launch_qr_lds(const float* A, int64_t batch, int n, int64_t as0, int6
                          hipStream_t stream);
 
 // Blocked path (qr_blocked.hip).
+// Copy columns [c0, c1) of A (any strides) into H (columns contiguous); c0 a
+// multiple of 64.
 hipError_t launch_copy_colmajor(const float* A, int64_t batch, int n, int64_t as0, int64_t as1, int64_t as2,
-                                float* H, int64_t hs0, int64_t ldh, hipStream_t stream);
+                                float* H, int64_t hs0, int64_t ldh, int c0, int c1, hipStream_t stream);
 // Panel width (32, or 16 above 2048 rows) and the tallest panel supported (qr_panel.hip).
 int panel_width_for(int m);
 // Panel width of the strip-resident path (64 or 32; T slots of 32 columns).

@@ -25,11 +25,11 @@ namespace fastqr {
 __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __restrict__ A, int64_t as0,
                                                                 int64_t as1, int64_t as2,
                                                                 float* __restrict__ H, int64_t hs0,
-                                                                int64_t ldh, int n, int ntile, bool vec) {
+                                                                int64_t ldh, int n, int ntile, int tj0, bool vec) {
   __shared__ float tile[64][65];
   const int64_t b = blockIdx.y;
   const int ti = blockIdx.x % ntile;
-  const int tj = blockIdx.x / ntile;
+  const int tj = tj0 + (int)(blockIdx.x / ntile);
   const float* Ab = A + b * as0;
   float* Hb = H + b * hs0;
   const int tid = threadIdx.x;
@@ -270,7 +270,7 @@ __device__ __forceinline__ void wy_update_item(float* __restrict__ H, int64_t hs
 // critical-path kernels on the other stream.
 template <int NW, int TPW, bool RES, bool VEC>
 __global__ void __launch_bounds__(NW * 64)
-__attribute__((amdgpu_waves_per_eu((TPW >= 2 && NW == 8) || (TPW >= 4 && NW <= 4) ? 2 : 4, 8)))
+__attribute__((amdgpu_waves_per_eu((TPW >= 2 && NW >= 4) || (TPW >= 4 && NW <= 4) ? 2 : 4, 8)))
 wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* __restrict__ Tws, int n, int k0,
                  int nb, int slot0, int nwy, int c_begin, int c_end, int hi_prio, int nstrips, int batch) {
   // updates on the critical path (the rest of a panel group, the next group's
@@ -290,12 +290,15 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
 // Host-side launchers
 // ---------------------------------------------------------------------------
 hipError_t launch_copy_colmajor(const float* A, int64_t batch, int n, int64_t as0, int64_t as1, int64_t as2,
-                                float* H, int64_t hs0, int64_t ldh, hipStream_t stream) {
+                                float* H, int64_t hs0, int64_t ldh, int c0, int c1, hipStream_t stream) {
+  if (c0 < 0 || (c0 & 63) != 0 || c1 > n) return hipErrorInvalidValue;
+  if (c1 <= c0) return hipSuccess;
   const int ntile = (n + 63) / 64;
+  const int tj0 = c0 / 64, ntj = (c1 - c0 + 63) / 64;
   const bool vec = as2 == 1 && (as1 & 3) == 0 && (as0 & 3) == 0 && ((uintptr_t)A & 15) == 0 && (ldh & 3) == 0 &&
                    (hs0 & 3) == 0 && ((uintptr_t)H & 15) == 0 && (n & 3) == 0;
-  hipLaunchKernelGGL(copy_to_colmajor_kernel, dim3(ntile * ntile, (unsigned)batch), dim3(256), 0, stream, A,
-                     as0, as1, as2, H, hs0, ldh, n, ntile, vec);
+  hipLaunchKernelGGL(copy_to_colmajor_kernel, dim3(ntile * ntj, (unsigned)batch), dim3(256), 0, stream, A,
+                     as0, as1, as2, H, hs0, ldh, n, ntile, tj0, vec);
   return hipGetLastError();
 }
 
@@ -341,13 +344,15 @@ hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, c
   // batches, narrow updates), and 4 per wave once the launch alone holds
   // about four waves per SIMD of the GPU.
   constexpr int64_t kWaveBudget = 4096;
-  // 16 waves (128 registers each) hold at most 2 tiles per wave without
-  // spilling; taller strips use 8 waves of up to 8 tiles.
+  // At most 8 waves: 16-wave workgroups (128 registers a wave) spill and have
+  // no room for the LDS transpose of V (measured on MI355X: 8 waves of 2-4
+  // tiles make 40 x 352 7% and 60 x 1024 3% faster); taller strips use 8
+  // waves of up to 8 tiles.
   int nw = 0, tpw = 0;
   for (int t = 1; t <= 4; t *= 2) {
     int w = 1;
     while (w * t < ntiles) w *= 2;
-    if (w <= (t <= 2 ? 16 : 8) && strips * batch * w <= kWaveBudget) {
+    if (w <= 8 && strips * batch * w <= kWaveBudget) {
       nw = w, tpw = t;
       break;
     }
@@ -375,19 +380,17 @@ hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, c
   FASTQR_WY(2, 1, true)
   FASTQR_WY(4, 1, true)
   FASTQR_WY(8, 1, true)
-  FASTQR_WY(16, 1, true)
   FASTQR_WY(1, 2, true)
   FASTQR_WY(2, 2, true)
   FASTQR_WY(4, 2, true)
   FASTQR_WY(8, 2, true)
-  FASTQR_WY(16, 2, true)
   FASTQR_WY(1, 4, true)
   FASTQR_WY(2, 4, true)
   FASTQR_WY(4, 4, true)
   FASTQR_WY(8, 4, true)
   FASTQR_WY(8, 8, true)
 #undef FASTQR_WY
-  // strips taller than 16 waves x 4 tiles: stream the tiles
+  // strips taller than 8 waves x 8 tiles: stream the tiles
   if (vec)
     hipLaunchKernelGGL((wy_update_kernel<16, 1, false, true>), grid_for(wy_update_kernel<16, 1, false, true>, 1024), dim3(16 * 64), 0, stream, H, hs0, ldh, Tws, n,
                        k0, nb, slot0, nwy, c_begin, c_end, prio, ns, nbatch);
