@@ -270,10 +270,60 @@ __global__ void __launch_bounds__(kSumWaves * 64) wyr_w_kernel(const float* __re
   store_acc(Wbuf + ((b * nstrips_w + s) * kWyrMaxBlk + blk) * 1024, W, lane);
 }
 
-template <int NBLK, bool VEC>
+// W of one strip formed by a single wave (the fused variant of the apply
+// kernel): the row-block partials summed in row-block order, four loads in
+// flight, then W = -T^T P as in wyr_w_kernel.
+template <int NBLK>
+__device__ __forceinline__ void wave_form_w(f32x16 (&W)[NBLK], const float* __restrict__ Ppart, int64_t b, int s,
+                                            int nstrips, int nrb, const float* __restrict__ Tb, int ldt, int k,
+                                            int lane) {
+  const int h = lane >> 5, l32 = lane & 31;
+  f32x16 P[NBLK];
+#pragma unroll
+  for (int blk = 0; blk < NBLK; ++blk) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) P[blk][j] = 0.0f;
+    int rb = 0;
+    for (; rb + 3 < nrb; rb += 4) {
+      f32x16 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = load_acc(Ppart + pp_index(b, s, rb + u, blk, nstrips, nrb), lane);
+#pragma unroll
+      for (int u = 0; u < 4; ++u) P[blk] += v[u];
+    }
+    for (; rb < nrb; ++rb) P[blk] += load_acc(Ppart + pp_index(b, s, rb, blk, nstrips, nrb), lane);
+  }
+#pragma unroll
+  for (int blk = 0; blk < NBLK; ++blk) {
+    f32x16 acc;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
+#pragma unroll
+    for (int bp = 0; bp <= blk; ++bp) {
+      float t[16];
+#pragma unroll
+      for (int j = 0; j < 16; ++j) {
+        const int kk = 32 * bp + acc_row(j, h);
+        const int cc = 32 * blk + l32;
+        t[j] = (kk < k && cc < k) ? Tb[kk * ldt + cc] : 0.0f;
+      }
+#pragma unroll
+      for (int j = 0; j < 16; ++j) acc = __builtin_amdgcn_mfma_f32_32x32x2f32(t[j], P[bp][j], acc, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) W[blk][j] = -acc[j];
+  }
+}
+
+// FW: W formed in the kernel from the partials (Ppart, strips s0 + s) and T
+// instead of read from Wbuf; every row block's wave repeats it, which costs
+// less than the separate W launch on the critical path.
+template <int NBLK, bool VEC, bool FW>
 __global__ void __launch_bounds__(64) wyr_apply_kernel(float* __restrict__ H, int64_t hs0, int ldh, int n, int kv,
                                                        int k, int c_begin, int c_end, int rows_per_blk,
-                                                       const float* __restrict__ Wbuf, int nstrips_w, int hi) {
+                                                       const float* __restrict__ Wbuf, int nstrips_w, int hi,
+                                                       const float* __restrict__ Ppart, int nstrips, int nrb, int s0,
+                                                       const float* __restrict__ Tsrc, int64_t t_stride, int ldt) {
   if (hi) __builtin_amdgcn_s_setprio(2);
   const int s = blockIdx.x, rb = blockIdx.y;
   const int64_t b = blockIdx.z;
@@ -284,8 +334,13 @@ __global__ void __launch_bounds__(64) wyr_apply_kernel(float* __restrict__ H, in
   const int r_lo = kv + rb * rows_per_blk;
   const int r_hi = min(n, r_lo + rows_per_blk);
   f32x16 W[NBLK];
+  if constexpr (FW) {
+    wave_form_w<NBLK>(W, Ppart, b, s0 + s, nstrips, nrb, Tsrc + b * t_stride, ldt, k, lane);
+  } else {
 #pragma unroll
-  for (int blk = 0; blk < NBLK; ++blk) W[blk] = load_acc(Wbuf + ((b * nstrips_w + s) * kWyrMaxBlk + blk) * 1024, lane);
+    for (int blk = 0; blk < NBLK; ++blk)
+      W[blk] = load_acc(Wbuf + ((b * nstrips_w + s) * kWyrMaxBlk + blk) * 1024, lane);
+  }
 
   auto load_v = [&](int r0, f32x16 (&v)[NBLK]) {
 #pragma unroll
@@ -384,8 +439,10 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
   }
   const int nx = nstrips - gram_strips;  // strips that are updated
   if (nx <= 0) return hipSuccess;
+  // critical-path updates form W inside the apply kernel (one launch fewer)
+  const bool fw = c.hi_prio;
   const dim3 gw((unsigned)nx, (unsigned)c.batch);
-  switch (nblk) {
+  if (!fw) switch (nblk) {
     case 1:
       hipLaunchKernelGGL((wyr_w_kernel<1>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
                          ldt, c.k, Wbuf, nx, hi);
@@ -406,14 +463,20 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
   if ((e = hipGetLastError()) != hipSuccess) return e;
   const int xc_begin = c.c_begin + 32 * gram_strips;
   const dim3 ga((unsigned)nx, (unsigned)nrb, (unsigned)c.batch);
+#define WYR_APPLY_FW(NB_, VEC_, FW_)                                                                               \
+  hipLaunchKernelGGL((wyr_apply_kernel<NB_, VEC_, FW_>), ga, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv, c.k, \
+                     xc_begin, c.c_end, c.rows_per_blk, Wbuf, nx, hi, Ppart, nstrips, nrb, gram_strips, Tsrc,      \
+                     t_stride, ldt)
 #define WYR_APPLY(NB_)                                                                                             \
   do {                                                                                                             \
-    if (c.vec)                                                                                                     \
-      hipLaunchKernelGGL((wyr_apply_kernel<NB_, true>), ga, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv, c.k, \
-                         xc_begin, c.c_end, c.rows_per_blk, Wbuf, nx, hi);                                             \
+    if (c.vec && fw)                                                                                               \
+      WYR_APPLY_FW(NB_, true, true);                                                                               \
+    else if (c.vec)                                                                                                \
+      WYR_APPLY_FW(NB_, true, false);                                                                              \
+    else if (fw)                                                                                                   \
+      WYR_APPLY_FW(NB_, false, true);                                                                              \
     else                                                                                                           \
-      hipLaunchKernelGGL((wyr_apply_kernel<NB_, false>), ga, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv,    \
-                         c.k, xc_begin, c.c_end, c.rows_per_blk, Wbuf, nx, hi);                                        \
+      WYR_APPLY_FW(NB_, false, false);                                                                             \
   } while (0)
   switch (nblk) {
     case 1: WYR_APPLY(1); break;
@@ -422,6 +485,7 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
     default: WYR_APPLY(4); break;
   }
 #undef WYR_APPLY
+#undef WYR_APPLY_FW
   return hipGetLastError();
 }
 
