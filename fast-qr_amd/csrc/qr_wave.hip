@@ -8,8 +8,8 @@
 // of v_mfma_f32_16x16x4f32: lane (kq = lane/16, cn = lane%16) holds, in
 // X[tr][tc], rows 16tr + 4kq .. +3 of column 16tc + cn.  A 16-lane row of the
 // wave therefore holds four rows of all sixteen columns of a tile column, and
-// at step j the pivot column is broadcast to every lane of its row with one
-// DPP row_newbcast move per register.  Each lane then forms, for its own
+// at step j the pivot column is broadcast to every lane of its row by the DPP
+// row_newbcast modifier of the FMAs that use it.  Each lane then forms, for its own
 // columns c >= j,
 //     g_c = sum_{r>j} x_r a_r[c]        (c == j gives sigma)
 // over its four rows per tile; the four 16-lane rows are summed with
@@ -24,10 +24,71 @@ namespace fastqr {
 
 namespace {
 
-// lane J of this lane's 16-lane row
-template <int J>
-__device__ __forceinline__ float row_bcast(float v) {
-  return __int_as_float(__builtin_amdgcn_mov_dpp(__float_as_int(v), 0x150 + J, 0xF, 0xF, false));
+// 16-lane row R of v in every row: v_permlane32_swap(v, v) returns rows
+// (0,1,0,1) and (2,3,2,3); v_permlane16_swap(w, w) then returns (w0,w0,w2,w2)
+// and (w1,w1,w3,w3).  Two exchanges, no selects, no arithmetic.
+template <int R>
+__device__ __forceinline__ float row_broadcast(float v) {
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(v), __float_as_uint(v), false, false);
+  const unsigned w = R < 2 ? h[0] : h[1];
+  const auto q = __builtin_amdgcn_permlane16_swap(w, w, false, false);
+  return __uint_as_float((R & 1) ? q[1] : q[0]);
+}
+
+// DPP rows (16-lane groups kq) whose register i holds a row below row JJ of
+// the tile (rows 4kq + i); all four rows for a tile below the diagonal tile.
+constexpr int below_rows(int jj, int i, bool diag) {
+  int m = 0;
+  for (int kq = 0; kq < 4; ++kq)
+    if (!diag || 4 * kq + i > jj) m |= 1 << kq;
+  return m;
+}
+
+// The pivot broadcast (row_newbcast:J, lane J of each 16-lane row) fused into
+// v_fmac_f32_dpp, and the rows at or above the pivot skipped by the DPP row
+// mask (a masked lane keeps its destination).  The compiler does not fold a
+// row_newbcast move into an FMA, so the forms are written out; each block
+// opens with the two wait states a DPP read needs after a VALU write of its
+// source register ("s_nop 1"), which the compiler cannot see across asm.
+//   g0 += b(x0) y0 + b(x2) y2,  g1 += b(x1) y1 + b(x3) y3
+template <int J, int M0, int M1, int M2, int M3>
+__device__ __forceinline__ void bdot4(float& g0, float& g1, const f32x4& x, const f32x4& y) {
+  asm("s_nop 1\n\t"
+      "v_fmac_f32_dpp %0, %2, %6 row_newbcast:%c10 row_mask:%c11 bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %3, %7 row_newbcast:%c10 row_mask:%c12 bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %0, %4, %8 row_newbcast:%c10 row_mask:%c13 bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %5, %9 row_newbcast:%c10 row_mask:%c14 bank_mask:0xf"
+      : "+v"(g0), "+v"(g1)
+      : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(y[0]), "v"(y[1]), "v"(y[2]), "v"(y[3]), "i"(J), "i"(M0),
+        "i"(M1), "i"(M2), "i"(M3));
+}
+
+//   d_i += b(x_i) a
+template <int J, int M0, int M1, int M2, int M3>
+__device__ __forceinline__ void baxpy4(f32x4& d, const f32x4& x, float a) {
+  float d0 = d[0], d1 = d[1], d2 = d[2], d3 = d[3];
+  asm("s_nop 1\n\t"
+      "v_fmac_f32_dpp %0, %4, %8 row_newbcast:%c9 row_mask:%c10 bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %5, %8 row_newbcast:%c9 row_mask:%c11 bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %2, %6, %8 row_newbcast:%c9 row_mask:%c12 bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %3, %7, %8 row_newbcast:%c9 row_mask:%c13 bank_mask:0xf"
+      : "+v"(d0), "+v"(d1), "+v"(d2), "+v"(d3)
+      : "v"(x[0]), "v"(x[1]), "v"(x[2]), "v"(x[3]), "v"(a), "i"(J), "i"(M0), "i"(M1), "i"(M2), "i"(M3));
+  d = f32x4{d0, d1, d2, d3};
+}
+
+//   x_i += b(x_i) a  (the pivot column's own tile: lane J keeps its value, a = 0 there)
+template <int J, int M0, int M1, int M2, int M3>
+__device__ __forceinline__ void baxpy4_self(f32x4& x, float a) {
+  float x0 = x[0], x1 = x[1], x2 = x[2], x3 = x[3];
+  asm("s_nop 1\n\t"
+      "v_fmac_f32_dpp %0, %0, %4 row_newbcast:%c5 row_mask:%c6 bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %1, %4 row_newbcast:%c5 row_mask:%c7 bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %2, %2, %4 row_newbcast:%c5 row_mask:%c8 bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %3, %3, %4 row_newbcast:%c5 row_mask:%c9 bank_mask:0xf"
+      : "+v"(x0), "+v"(x1), "+v"(x2), "+v"(x3)
+      : "v"(a), "i"(J), "i"(M0), "i"(M1), "i"(M2), "i"(M3));
+  x = f32x4{x0, x1, x2, x3};
 }
 
 template <int... I>
@@ -52,40 +113,29 @@ struct WaveQR {
   template <int J>
   __device__ __forceinline__ void step() {
     constexpr int TJ = J / 16, JJ = J % 16, KQJ = JJ / 4, IJ = JJ % 4;
-    // row J of every column: register IJ of tile row TJ in DPP row KQJ, zero
-    // in the other rows, so the cross-row sums that total the dot products
-    // also broadcast it to every lane
+    // row J of every column (register IJ of tile row TJ in DPP row KQJ),
+    // broadcast to every row; alpha straight from its owner lane
     float rt[NT];
 #pragma unroll
-    for (int tc = TJ; tc < NT; ++tc) rt[tc] = (kq == KQJ) ? X[TJ][tc][IJ] : 0.0f;
-    // pivot column, broadcast along each 16-lane row; rows <= J masked
-    f32x4 xb[NT];
-#pragma unroll
-    for (int tr = TJ; tr < NT; ++tr) {
-#pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const float v = row_bcast<JJ>(X[tr][TJ][i]);
-        xb[tr][i] = (tr > TJ || 4 * kq + i > JJ) ? v : 0.0f;
-      }
-    }
+    for (int tc = TJ; tc < NT; ++tc) rt[tc] = row_broadcast<KQJ>(X[TJ][tc][IJ]);
+    const float alpha = readlane(X[TJ][TJ][IJ], 16 * KQJ + JJ);
+    // g_c = sum_{r > J} x_r a_r[c]: the pivot column broadcast along each
+    // 16-lane row, rows <= J skipped by the row masks of the diagonal tile row
+    constexpr int D0 = below_rows(JJ, 0, true), D1 = below_rows(JJ, 1, true);
+    constexpr int D2 = below_rows(JJ, 2, true), D3 = below_rows(JJ, 3, true);
     float g[NT];
 #pragma unroll
     for (int tc = TJ; tc < NT; ++tc) {
       float a0 = 0.0f, a1 = 0.0f;
+      bdot4<JJ, D0, D1, D2, D3>(a0, a1, X[TJ][TJ], X[TJ][tc]);
 #pragma unroll
-      for (int tr = TJ; tr < NT; ++tr) {
-        a0 = fmaf(xb[tr][0], X[tr][tc][0], a0);
-        a1 = fmaf(xb[tr][1], X[tr][tc][1], a1);
-        a0 = fmaf(xb[tr][2], X[tr][tc][2], a0);
-        a1 = fmaf(xb[tr][3], X[tr][tc][3], a1);
-      }
+      for (int tr = TJ + 1; tr < NT; ++tr) bdot4<JJ, 15, 15, 15, 15>(a0, a1, X[tr][TJ], X[tr][tc]);
       g[tc] = a0 + a1;
     }
 #pragma unroll
-    for (int tc = TJ; tc < NT; ++tc) g[tc] = xor16_sum(g[tc]), rt[tc] = xor16_sum(rt[tc]);
+    for (int tc = TJ; tc < NT; ++tc) g[tc] = xor16_sum(g[tc]);
 #pragma unroll
-    for (int tc = TJ; tc < NT; ++tc) g[tc] = xor32_sum(g[tc]), rt[tc] = xor32_sum(rt[tc]);
-    const float alpha = readlane(rt[TJ], JJ);
+    for (int tc = TJ; tc < NT; ++tc) g[tc] = xor32_sum(g[tc]);
     // lane JJ holds column J's totals
     const float sigma = readlane(g[TJ], JJ);
     const Reflector rf = make_reflector_sel(alpha, sigma);
@@ -100,18 +150,24 @@ struct WaveQR {
     // the pivot column (s = 0) keeps its unscaled x: v = x * inv is applied
     // once after the last step
 #pragma unroll
-    for (int tr = TJ; tr < NT; ++tr) {
+    for (int tc = TJ + 1; tc < NT; ++tc) {
+      baxpy4<JJ, D0, D1, D2, D3>(X[TJ][tc], X[TJ][TJ], alp[tc]);
+#pragma unroll
+      for (int tr = TJ + 1; tr < NT; ++tr) baxpy4<JJ, 15, 15, 15, 15>(X[tr][tc], X[tr][TJ], alp[tc]);
+    }
+    baxpy4_self<JJ, D0, D1, D2, D3>(X[TJ][TJ], alp[TJ]);
+#pragma unroll
+    for (int tr = TJ + 1; tr < NT; ++tr) baxpy4_self<JJ, 15, 15, 15, 15>(X[tr][TJ], alp[TJ]);
+    // row J: a_J[c] - s_c for c > J, beta on the diagonal
+    {
+      const bool row_j = kq == KQJ;  // selects, not a branch: a branch here makes
+                                     // the compiler copy whole register quads
 #pragma unroll
       for (int tc = TJ; tc < NT; ++tc) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i) X[tr][tc][i] = fmaf(alp[tc], xb[tr][i], X[tr][tc][i]);
+        const float a = X[TJ][tc][IJ];
+        const float nv = (tc == TJ && cn == JJ) ? rf.beta : a - s[tc];
+        X[TJ][tc][IJ] = row_j ? nv : a;
       }
-    }
-    // row J: a_J[c] - s_c for c > J, beta on the diagonal
-    if (kq == KQJ) {
-#pragma unroll
-      for (int tc = TJ; tc < NT; ++tc)
-        X[TJ][tc][IJ] = (tc == TJ && cn == JJ) ? rf.beta : X[TJ][tc][IJ] - s[tc];
     }
     tv[TJ] = (cn == JJ) ? rf.tau : tv[TJ];
     inv[TJ] = (cn == JJ) ? rf.inv : inv[TJ];
