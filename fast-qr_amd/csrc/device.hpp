@@ -83,6 +83,23 @@ __device__ __forceinline__ float xor16_sum(float v) {
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
 
+// Totals over the four 16-lane rows of two values at once, in every lane
+// (a(l) + a(l^16) + a(l^32) + a(l^48), same for b, in the same order of
+// additions as xor16_sum then xor32_sum).  v_permlane16_swap(a, b) leaves
+// rows (a0,b0,a2,b2) and (a1,b1,a3,b3), whose sum holds the a pairs in rows 0
+// and 2 and the b pairs in rows 1 and 3; a v_permlane32_swap of that with
+// itself adds the halves, and a v_permlane16_swap with itself spreads row 0
+// (a) and row 1 (b) to all rows: three exchanges instead of four.
+__device__ __forceinline__ void pair_row_sums(float& a, float& b) {
+  const auto p = __builtin_amdgcn_permlane16_swap(__float_as_uint(a), __float_as_uint(b), false, false);
+  const float s = __uint_as_float(p[0]) + __uint_as_float(p[1]);
+  const auto h = __builtin_amdgcn_permlane32_swap(__float_as_uint(s), __float_as_uint(s), false, false);
+  const float t = __uint_as_float(h[0]) + __uint_as_float(h[1]);
+  const auto q = __builtin_amdgcn_permlane16_swap(__float_as_uint(t), __float_as_uint(t), false, false);
+  a = __uint_as_float(q[0]);
+  b = __uint_as_float(q[1]);
+}
+
 // Reflector without branches (alpha, sigma wave-uniform): the same values as
 // make_reflector, selected instead of branched on so a column step has no
 // scalar branch.

@@ -184,10 +184,7 @@ __device__ __forceinline__ void panel_body(IO& io, int m, int tid) {
           // row JG of my column: tile T_OWN of wave W_OWN, register JJ % 4 of lane row JJ / 4
           const bool row_owner = (wave == W_OWN) && (kq == JJ / 4);
           float rowt = row_owner ? X[BLK][T_OWN][JJ & 3] : 0.0f;
-          tot = xor16_sum(tot);
-          rowt = xor16_sum(rowt);
-          tot = xor32_sum(tot);
-          rowt = xor32_sum(rowt);
+          pair_row_sums(tot, rowt);
           if constexpr (NW > 1) {
             if (kq == 0) red[PAR][cn][wave] = make_float2(tot, rowt);
             io.barrier();

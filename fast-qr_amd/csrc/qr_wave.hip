@@ -133,9 +133,8 @@ struct WaveQR {
       g[tc] = a0 + a1;
     }
 #pragma unroll
-    for (int tc = TJ; tc < NT; ++tc) g[tc] = xor16_sum(g[tc]);
-#pragma unroll
-    for (int tc = TJ; tc < NT; ++tc) g[tc] = xor32_sum(g[tc]);
+    for (int tc = TJ; tc + 1 < NT; tc += 2) pair_row_sums(g[tc], g[tc + 1]);
+    if constexpr (((NT - TJ) & 1) != 0) g[NT - 1] = xor32_sum(xor16_sum(g[NT - 1]));
     // lane JJ holds column J's totals
     const float sigma = readlane(g[TJ], JJ);
     const Reflector rf = make_reflector_sel(alpha, sigma);
