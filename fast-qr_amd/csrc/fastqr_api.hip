@@ -431,15 +431,14 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   // The wide update that overlaps the next group's panels leaves one CU per
   // matrix to them when the batch is smaller than the GPU: each panel
   // workgroup needs most of a CU's registers and would otherwise wait for a
-  // CU to drain behind the update's workgroups.  Small batches leave four
-  // (measured on MI355X: 8 x 2048 5% faster; eight per matrix gain nothing
-  // more).
+  // CU to drain behind the update's workgroups.  Small batches leave four, so
+  // the narrow update after each panel (one workgroup per matrix and strip)
+  // runs beside the wide update too; the wide update has slack (measured on
+  // MI355X: 8 x 2048 5% faster; eight CUs per matrix gain nothing more).
   int num_cus = 0, dev = 0;
   if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&num_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     num_cus = 0;
-  // (the narrow update after each panel, one workgroup per matrix and strip,
-  // then runs beside the wide update as well; the wide update has slack)
   int rest_cus = 0;
   if (num_cus > 0 && batch < num_cus / 2)
     rest_cus = (4 * batch <= num_cus / 2) ? num_cus - 4 * (int)batch : num_cus - (int)batch;
