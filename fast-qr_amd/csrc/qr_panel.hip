@@ -38,8 +38,12 @@ struct GlobalPanelIO {
 
 }  // namespace
 
+// Occupancy: (4, 8, 2) is held to 168 registers (three waves per SIMD, three
+// workgroups per CU), so 640 matrices of 512 rows run in one round on 256 CUs
+// instead of two.
 template <int NW, int TPW, int NBLK, bool VEC>
-__global__ void __launch_bounds__(NW * 64) __attribute__((amdgpu_waves_per_eu((NW + 3) / 4, 8)))
+__global__ void __launch_bounds__(NW * 64)
+__attribute__((amdgpu_waves_per_eu((NW == 4 && TPW == 8 && NBLK == 2 && VEC) ? 3 : (NW + 3) / 4, 8)))
 panel_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, float* __restrict__ tau, int64_t ts0, int64_t ts1,
              float* __restrict__ Tws, int n, int k0, int slot) {
   // the panel is the critical path: its waves win issue arbitration against
