@@ -394,7 +394,7 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   // together to the columns right of it.  Look-ahead: that wide update is
   // split into the next group's columns (first) and the rest; the next
   // group's panels run on a side stream while the rest is updated on the
-  // caller's stream.  T slots alternate between two banks by group parity.
+  // caller's stream.  T slots rotate over three banks.
   struct Group {
     int g0, pw, g_end, slot_base;
   };
@@ -402,7 +402,7 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   std::vector<Group> groups;
   for (int g0 = 0, gi = 0; g0 < ni; ++gi) {
     const int g_end = (g0 + fastqr::kMaxWY * kTw < ni) ? g0 + fastqr::kMaxWY * kTw : ni;
-    groups.push_back(Group{g0, fastqr::panel_width_wide(ni - g0, batch), g_end, (gi & 1) * fastqr::kMaxWY});
+    groups.push_back(Group{g0, fastqr::panel_width_wide(ni - g0, batch), g_end, (gi % 3) * fastqr::kMaxWY});
     g0 = g_end;
   }
   auto run_panels = [&](const Group& G, hipStream_t st) -> hipError_t {
@@ -468,12 +468,13 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
     return FASTQR_OK;
   }
   // The panels and the look-ahead updates (the critical path) run in order on
-  // the side stream.  The wide update of each group's remaining columns runs
-  // on the caller's stream after the group's look-ahead update (not beside
-  // it: the look-ahead is on the critical path), overlapping the next
-  // group's panels.  The look-ahead of group g waits for the wide update of
-  // group g-1, which produced the columns it reads (and last read the T bank
-  // that group g+1's panels overwrite).
+  // the side stream.  The wide update of group g runs on the caller's stream
+  // after g's look-ahead update (not beside it: the look-ahead is on the
+  // critical path), overlapping the next group's panels, in two parts: first
+  // the columns of group g+2, which the next look-ahead update reads (it waits
+  // for that part only), then everything right of them.  T slots rotate over
+  // three banks: group g+1's panels overwrite the bank of group g-2, so they
+  // wait for g-2's wide update to end (long done in practice).
   const hipStream_t side = aux->side;
   auto record = [&](hipStream_t st) -> hipEvent_t {
     hipEvent_t evt = aux->take();
@@ -485,20 +486,28 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   if ((e = hipStreamWaitEvent(side, ev, 0)) != hipSuccess) return hip_fail(e, "stream join");
   if ((e = run_panels(groups[0], side)) != hipSuccess) return hip_fail(e, "panel launch");
   if ((e = copy_cols(c_first, ni)) != hipSuccess) return hip_fail(e, "copy launch");
-  // the first look-ahead waits for the copy (then for each wide update)
-  hipEvent_t ev_rest = c_first < ni ? record(stream) : nullptr;
-  if (c_first < ni && !ev_rest) return fail(FASTQR_EINVAL, "cannot record HIP events");
+  // columns of the next look-ahead update ready (first: the copy)
+  hipEvent_t ev_near = c_first < ni ? record(stream) : nullptr;
+  if (c_first < ni && !ev_near) return fail(FASTQR_EINVAL, "cannot record HIP events");
+  std::vector<hipEvent_t> ev_rest(groups.size(), nullptr);  // group g's wide update ended
   for (size_t g = 0; g + 1 < groups.size(); ++g) {
     const Group& G = groups[g];
     const Group& Nx = groups[g + 1];
-    if (ev_rest && (e = hipStreamWaitEvent(side, ev_rest, 0)) != hipSuccess) return hip_fail(e, "stream join");
+    if (ev_near && (e = hipStreamWaitEvent(side, ev_near, 0)) != hipSuccess) return hip_fail(e, "stream join");
     if ((e = run_update(G, Nx.g0, Nx.g_end, true, side)) != hipSuccess) return hip_fail(e, "update launch");
     hipEvent_t ev_la = record(side);
     if (!ev_la) return fail(FASTQR_EINVAL, "cannot record HIP events");
+    if (g >= 2 && (e = hipStreamWaitEvent(side, ev_rest[g - 2], 0)) != hipSuccess) return hip_fail(e, "stream join");
     if ((e = run_panels(Nx, side)) != hipSuccess) return hip_fail(e, "panel launch");
     if ((e = hipStreamWaitEvent(stream, ev_la, 0)) != hipSuccess) return hip_fail(e, "stream join");
-    if ((e = run_update(G, Nx.g_end, ni, false, stream)) != hipSuccess) return hip_fail(e, "update launch");
-    if (!(ev_rest = record(stream))) return fail(FASTQR_EINVAL, "cannot record HIP events");
+    ev_near = nullptr;
+    if (g + 2 < groups.size()) {
+      const Group& N2 = groups[g + 2];
+      if ((e = run_update(G, N2.g0, N2.g_end, false, stream)) != hipSuccess) return hip_fail(e, "update launch");
+      if (!(ev_near = record(stream))) return fail(FASTQR_EINVAL, "cannot record HIP events");
+      if ((e = run_update(G, N2.g_end, ni, false, stream)) != hipSuccess) return hip_fail(e, "update launch");
+    }
+    if (!(ev_rest[g] = record(stream))) return fail(FASTQR_EINVAL, "cannot record HIP events");
   }
   hipEvent_t ev_end = record(side);
   if (!ev_end) return fail(FASTQR_EINVAL, "cannot record HIP events");

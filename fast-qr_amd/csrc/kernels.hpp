@@ -77,9 +77,9 @@ size_t wyr_workspace_floats(int64_t batch, int n);
 
 // Panels per group: the wide trailing update applies this many transforms at once.
 constexpr int kMaxWY = 4;
-// T-factor slots per matrix in the workspace (32 x 32 floats each): two
-// groups' worth, so one group's panels can run while the previous group's
-// transforms are still being applied.
-constexpr int kMaxSlots = 2 * kMaxWY;
+// T-factor slots per matrix in the workspace (32 x 32 floats each): three
+// groups' worth, so a group's panels can run while the wide updates of the
+// two groups before it are still being applied.
+constexpr int kMaxSlots = 3 * kMaxWY;
 
 }  // namespace fastqr
