@@ -395,13 +395,20 @@ __device__ __forceinline__ void panel_body(IO& io, int m, int tid) {
   io.barrier();
 
   // write the panel, T (one 32 x 32 slot per 32 columns; a 16-column panel
-  // fills the upper-left quarter of one slot) and tau
+  // fills the upper-left quarter of one slot) and tau.  For scalar loads and
+  // for 16- and 32-column panels the lane's row and column go through an
+  // opaque copy: the store offsets and bounds are then recomputed here instead
+  // of being kept live (spilled, with scalar loads) since the loads.  64- and
+  // 128-column panels keep them (measured on MI355X: 40 x 352 3% slower
+  // otherwise).
+  int kq_s = kq, cn_s = cn;
+  if constexpr (!VEC || NBLK <= 2) asm volatile("" : "+v"(kq_s), "+v"(cn_s));
 #pragma unroll
   for (int blk = 0; blk < NBLK; ++blk) {
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
-      const int r = 16 * (wave + NW * t) + 4 * kq;
-      const int c = 16 * blk + cn;
+      const int r = 16 * (wave + NW * t) + 4 * kq_s;
+      const int c = 16 * blk + cn_s;
       if constexpr (VEC) {
         io.store4(r, c, c < w && r < m, X[blk][t]);
       } else {
