@@ -124,17 +124,31 @@ __device__ __forceinline__ void wy_update_item(float* __restrict__ H, int64_t hs
   auto Pp = [&](int wv, int j) -> float* { return &Wreg[wv][j * 64]; };
   auto VTs = [&](int wv) { return reinterpret_cast<float (*)[36]>(&Wreg[wv][0]); };
 
-  for (int idx = threadIdx.x; idx < nwy * 32 * 32; idx += NW * 64) {
-    const int i = idx >> 10, r = (idx >> 5) & 31, cc = idx & 31;
-    Ts[i][r][cc] = (r < nb && cc < nb) ? Tws[((b * kMaxSlots + slot0 + i) * 32 + r) * 32 + cc] : 0.0f;
-  }
-
+  // The strip's tiles first, then the T factors with a chunk of loads in
+  // flight before their LDS writes: the latencies overlap instead of one
+  // global load per LDS write in turn.
   f32x16 X[TPW];
   if constexpr (RES) {
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       const int rt = wave + NW * t;
       X[t] = tile_load<VEC>(M, k0 + 32 * rt, col, colok && rt < ntiles, h);
+    }
+  }
+  constexpr int kTChunk = 8;
+  for (int base = threadIdx.x; base < nwy * 32 * 32; base += kTChunk * NW * 64) {
+    float tv[kTChunk];
+#pragma unroll
+    for (int u = 0; u < kTChunk; ++u) {
+      const int idx = base + u * NW * 64;
+      const int i = idx >> 10, r = (idx >> 5) & 31, cc = idx & 31;
+      tv[u] = (idx < nwy * 32 * 32 && r < nb && cc < nb) ? Tws[((b * kMaxSlots + slot0 + i) * 32 + r) * 32 + cc]
+                                                         : 0.0f;
+    }
+#pragma unroll
+    for (int u = 0; u < kTChunk; ++u) {
+      const int idx = base + u * NW * 64;
+      if (idx < nwy * 32 * 32) Ts[idx >> 10][(idx >> 5) & 31][idx & 31] = tv[u];
     }
   }
   __syncthreads();
