@@ -177,40 +177,71 @@ __global__ void __launch_bounds__(1024) wyr_tg_kernel(const float* __restrict__ 
   __shared__ float Ts[kWyrMaxK][kWyrMaxK + 1];
   __shared__ float Mt[kWyrMaxK][33];
   const int nblk = (k + 31) / 32;
-  // block (blk, s) of G = V_blk^T V_s, accumulator layout
-  for (int idx = tid; idx < nblk * nblk * 1024; idx += 1024) {
+  // block (blk, s) of G = V_blk^T V_s, accumulator layout; the loads of a
+  // thread's (up to 16) elements are all in flight before the LDS writes
+  constexpr int kG = kWyrMaxBlk * kWyrMaxBlk;
+  float gv[kG];
+#pragma unroll
+  for (int u = 0; u < kG; ++u) {
+    const int idx = tid + u * 1024;
     const int lane = idx & 63, j = (idx >> 6) & 15, pair = idx >> 10;
     const int blk = pair % nblk, s = pair / nblk;
-    Gs[32 * blk + acc_row(j, lane >> 5)][32 * s + (lane & 31)] =
-        Gsum[((b * kWyrMaxBlk + blk) * kWyrMaxBlk + s) * 1024 + j * 64 + lane];
+    gv[u] = (idx < nblk * nblk * 1024) ? Gsum[((b * kWyrMaxBlk + blk) * kWyrMaxBlk + s) * 1024 + j * 64 + lane] : 0.0f;
+  }
+  // the panels' T factors on the diagonal (nb * nb <= 1024: one element per
+  // thread and panel)
+  float tv[kWyrMaxK / 16];
+#pragma unroll
+  for (int i = 0; i < kWyrMaxK / 16; ++i) {
+    const int r = tid / nb, c = tid % nb;
+    tv[i] = (i < q && tid < nb * nb && i * nb + r < k && i * nb + c < k)
+                ? Tws[(b * kMaxSlots + slot0 + i) * 1024 + r * 32 + c]
+                : 0.0f;
+  }
+#pragma unroll
+  for (int u = 0; u < kG; ++u) {
+    const int idx = tid + u * 1024;
+    const int lane = idx & 63, j = (idx >> 6) & 15, pair = idx >> 10;
+    const int blk = pair % nblk, s = pair / nblk;
+    if (idx < nblk * nblk * 1024) Gs[32 * blk + acc_row(j, lane >> 5)][32 * s + (lane & 31)] = gv[u];
   }
   for (int idx = tid; idx < kWyrMaxK * kWyrMaxK; idx += 1024) Ts[idx / kWyrMaxK][idx % kWyrMaxK] = 0.0f;
   __syncthreads();
-  for (int i = 0; i < q; ++i) {
-    const float* Tp = Tws + (b * kMaxSlots + slot0 + i) * 1024;
-    for (int idx = tid; idx < nb * nb; idx += 1024) {
-      const int r = idx / nb, c = idx % nb;
-      if (i * nb + r < k && i * nb + c < k) Ts[i * nb + r][i * nb + c] = Tp[r * 32 + c];
-    }
+#pragma unroll
+  for (int i = 0; i < kWyrMaxK / 16; ++i) {
+    const int r = tid / nb, c = tid % nb;
+    if (i < q && tid < nb * nb && i * nb + r < k && i * nb + c < k) Ts[i * nb + r][i * nb + c] = tv[i];
   }
   __syncthreads();
+  // T join, one panel at a time; the dot products run over four partial sums
+  // so their LDS reads overlap
   for (int j = 1; j < q; ++j) {
     const int c0 = j * nb;
     if (c0 >= k) break;
     // Mt = G[0:c0, c0:c0+nb] T_j
     for (int idx = tid; idx < c0 * nb; idx += 1024) {
       const int r = idx / nb, c = idx % nb;
-      float acc = 0.0f;
-      for (int p = 0; p <= c; ++p) acc = fmaf(Gs[r][c0 + p], Ts[c0 + p][c0 + c], acc);
-      Mt[r][c] = acc;
+      float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      int p = 0;
+      for (; p + 3 <= c; p += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) a[u] = fmaf(Gs[r][c0 + p + u], Ts[c0 + p + u][c0 + c], a[u]);
+      }
+      for (; p <= c; ++p) a[0] = fmaf(Gs[r][c0 + p], Ts[c0 + p][c0 + c], a[0]);
+      Mt[r][c] = (a[0] + a[1]) + (a[2] + a[3]);
     }
     __syncthreads();
     // T[0:c0, c0:c0+nb] = -T[0:c0, 0:c0] Mt   (T upper triangular)
     for (int idx = tid; idx < c0 * nb; idx += 1024) {
       const int r = idx / nb, c = idx % nb;
-      float acc = 0.0f;
-      for (int p = r; p < c0; ++p) acc = fmaf(Ts[r][p], Mt[p][c], acc);
-      Ts[r][c0 + c] = -acc;
+      float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+      int p = r;
+      for (; p + 4 <= c0; p += 4) {
+#pragma unroll
+        for (int u = 0; u < 4; ++u) a[u] = fmaf(Ts[r][p + u], Mt[p + u][c], a[u]);
+      }
+      for (; p < c0; ++p) a[0] = fmaf(Ts[r][p], Mt[p][c], a[0]);
+      Ts[r][c0 + c] = -((a[0] + a[1]) + (a[2] + a[3]));
     }
     __syncthreads();
   }
