@@ -21,6 +21,9 @@ import torch
 from ._lib import env_flag
 
 _OUTPUT_CACHE: dict[tuple, tuple[weakref.ref, torch.Tensor]] = {}
+# (H, tau) pairs already handed out by allocate_h_tau, one dictionary lookup
+# per call; the tensors are the per-kind cache entries above
+_PAIR_CACHE: dict[tuple, tuple[weakref.ref, torch.Tensor, torch.Tensor]] = {}
 _SCRATCH: dict[tuple, torch.Tensor] = {}
 
 
@@ -78,8 +81,21 @@ def allocate_tau(batch: int, n: int, data: torch.Tensor, *, zero: bool = False,
 
 def allocate_h_tau(batch: int, n: int, data: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
     enabled = output_cache_enabled()
-    return (allocate_column_major_H(batch, n, data, cache_enabled=enabled),
-            allocate_tau(batch, n, data, cache_enabled=enabled))
+    if not enabled:
+        return (allocate_column_major_H(batch, n, data, cache_enabled=False),
+                allocate_tau(batch, n, data, cache_enabled=False))
+    key = (id(data), batch, n, data.get_device())
+    hit = _PAIR_CACHE.get(key)
+    if hit is not None and hit[0]() is data:
+        return hit[1], hit[2]
+    h = allocate_column_major_H(batch, n, data, cache_enabled=True)
+    tau = allocate_tau(batch, n, data, cache_enabled=True)
+    try:
+        ref = weakref.ref(data, lambda _r, k=key: _PAIR_CACHE.pop(k, None))
+    except TypeError:
+        return h, tau
+    _PAIR_CACHE[key] = (ref, h, tau)
+    return h, tau
 
 
 def scratch(device: torch.device, stream_ptr: int, nbytes: int) -> torch.Tensor | None:
@@ -96,4 +112,5 @@ def scratch(device: torch.device, stream_ptr: int, nbytes: int) -> torch.Tensor 
 
 def clear() -> None:
     _OUTPUT_CACHE.clear()
+    _PAIR_CACHE.clear()
     _SCRATCH.clear()
