@@ -42,6 +42,15 @@ constexpr int64_t kRowSplitMinN = 2049;
 
 bool use_rowsplit(int64_t /*batch*/, int64_t n) { return n >= kRowSplitMinN; }
 
+// Strip-resident path, small batches of tall matrices (8 x 2048): the narrow
+// update after a 32-column panel taller than kWyrNarrowMinRows runs on the
+// row-split kernels (partial products over row blocks, then the apply), which
+// spread it over hundreds of one-wave workgroups instead of one workgroup per
+// (matrix, strip).  Its partials and W need scratch beyond the T slots.
+constexpr int64_t kWyrNarrowMaxBatch = 16;
+constexpr int kWyrNarrowMinRows = 1024;
+bool use_wyr_narrow(int64_t batch, int64_t n) { return batch <= kWyrNarrowMaxBatch && n > kWyrNarrowMinRows; }
+
 bool ranges_overlap(const float* a, int64_t a_elems, const float* b, int64_t b_elems) {
   const uintptr_t a0 = (uintptr_t)a, a1 = a0 + (uintptr_t)a_elems * 4;
   const uintptr_t b0 = (uintptr_t)b, b1 = b0 + (uintptr_t)b_elems * 4;
@@ -304,6 +313,8 @@ size_t fastqr_workspace_bytes(int64_t batch, int64_t n) {
   size_t floats = (size_t)batch * fastqr::kMaxSlots * 32 * 32;
   if (use_rowsplit(batch, n))
     floats += 2 * (size_t)batch * fastqr::kWyrTgStride + 2 * fastqr::wyr_workspace_floats(batch, (int)n);
+  else if (use_wyr_narrow(batch, n))
+    floats += fastqr::wyr_workspace_floats(batch, (int)n);
   return (floats * sizeof(float) + 255) & ~(size_t)255;
 }
 
@@ -405,6 +416,10 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
     groups.push_back(Group{g0, fastqr::panel_width_wide(ni - g0, batch), g_end, (gi % 3) * fastqr::kMaxWY});
     g0 = g_end;
   }
+  // narrow updates on the row-split kernels (small batches of tall matrices);
+  // one scratch area: narrow updates run one at a time, on the side stream
+  const bool wyr_narrow = use_wyr_narrow(batch, n);
+  float* const wyr_scratch = Tws + (size_t)batch * fastqr::kMaxSlots * 1024;
   auto run_panels = [&](const Group& G, hipStream_t st) -> hipError_t {
     for (int pk = G.g0; pk < G.g_end; pk += G.pw) {
       const double m = ni - pk;
@@ -419,10 +434,31 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
       const int c0 = pk + wi;
       if (c0 < G.g_end) {
         const double c = G.g_end - c0;
-        err = timed(kUpdate, bd * 4.0 * m * wd * c, bd * (8.0 * m * c + 4.0 * m * wd), st, [&] {
-          return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, pk, kTw, slot, (wi + kTw - 1) / kTw, c0,
-                                          G.g_end, vec, true, 0, st);
-        });
+        if (wyr_narrow && wi <= kTw && ni - pk > kWyrNarrowMinRows) {
+          fastqr::WyrCall wc{};
+          wc.H = H;
+          wc.hs0 = h_s0;
+          wc.ldh = (int)h_s2;
+          wc.n = ni;
+          wc.batch = batch;
+          wc.kv = pk;
+          wc.k = wi;
+          wc.c_begin = c0;
+          wc.c_end = G.g_end;
+          wc.Tws = Tws;
+          wc.Tslot = Tws + slot * 1024;
+          wc.scratch = wyr_scratch;
+          wc.rows_per_blk = fastqr::wyr_rows_per_block(ni - pk, batch, G.g_end - c0);
+          wc.vec = vec;
+          wc.hi_prio = true;
+          err = timed(kUpdateRows, bd * 4.0 * m * wd * c, bd * (8.0 * m * c + 4.0 * m * wd), st,
+                      [&] { return fastqr::launch_wyr(wc, st); });
+        } else {
+          err = timed(kUpdate, bd * 4.0 * m * wd * c, bd * (8.0 * m * c + 4.0 * m * wd), st, [&] {
+            return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, pk, kTw, slot, (wi + kTw - 1) / kTw, c0,
+                                            G.g_end, vec, true, 0, st);
+          });
+        }
         if (err != hipSuccess) return err;
       }
     }
