@@ -75,6 +75,45 @@ __device__ __forceinline__ void bcast_axpy4(f32x4& x, float a0, float a1, float 
   x = f32x4{x0, x1, x2, x3};
 }
 
+// Two tiles per block (one "s_nop 1" for eight FMAs; inside a block no DPP
+// source is written):  g0,g1 += tile a as above, g2,g3 += tile b
+template <int J>
+__device__ __forceinline__ void bcast_dot8(float& g0, float& g1, float& g2, float& g3, f32x4 xa, f32x4 ya,
+                                           f32x4 xb, f32x4 yb) {
+  asm("s_nop 1\n\t"
+      "v_fmac_f32_dpp %0, %4, %8 row_newbcast:%c20 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %5, %9 row_newbcast:%c20 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %2, %12, %16 row_newbcast:%c20 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %3, %13, %17 row_newbcast:%c20 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %0, %6, %10 row_newbcast:%c20 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %7, %11 row_newbcast:%c20 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %2, %14, %18 row_newbcast:%c20 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %3, %15, %19 row_newbcast:%c20 row_mask:0xf bank_mask:0xf"
+      : "+v"(g0), "+v"(g1), "+v"(g2), "+v"(g3)
+      : "v"(xa[0]), "v"(xa[1]), "v"(xa[2]), "v"(xa[3]), "v"(ya[0]), "v"(ya[1]), "v"(ya[2]), "v"(ya[3]),
+        "v"(xb[0]), "v"(xb[1]), "v"(xb[2]), "v"(xb[3]), "v"(yb[0]), "v"(yb[1]), "v"(yb[2]), "v"(yb[3]), "i"(J));
+}
+
+// xa_i += b(xa_i) a,  xb_i += b(xb_i) a
+template <int J>
+__device__ __forceinline__ void bcast_axpy8(f32x4& xa, f32x4& xb, float a) {
+  float a0 = xa[0], a1 = xa[1], a2 = xa[2], a3 = xa[3];
+  float b0 = xb[0], b1 = xb[1], b2 = xb[2], b3 = xb[3];
+  asm("s_nop 1\n\t"
+      "v_fmac_f32_dpp %0, %0, %8 row_newbcast:%c9 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %1, %1, %8 row_newbcast:%c9 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %2, %2, %8 row_newbcast:%c9 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %3, %3, %8 row_newbcast:%c9 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %4, %4, %8 row_newbcast:%c9 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %5, %5, %8 row_newbcast:%c9 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %6, %6, %8 row_newbcast:%c9 row_mask:0xf bank_mask:0xf\n\t"
+      "v_fmac_f32_dpp %7, %7, %8 row_newbcast:%c9 row_mask:0xf bank_mask:0xf"
+      : "+v"(a0), "+v"(a1), "+v"(a2), "+v"(a3), "+v"(b0), "+v"(b1), "+v"(b2), "+v"(b3)
+      : "v"(a), "i"(J));
+  xa = f32x4{a0, a1, a2, a3};
+  xb = f32x4{b0, b1, b2, b3};
+}
+
 // acc += b(y) t,  b = row_newbcast:P
 template <int P>
 __device__ __forceinline__ void bcast_fma(float& acc, float y, float t) {
@@ -167,19 +206,21 @@ __device__ __forceinline__ void panel_body(IO& io, int m, int tid) {
           if (JG >= w) return;
           constexpr int PAR = JJ & 1;
           float g[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+          // tiles t < TD may hold rows <= JG (masked); the rest two per block
+          constexpr int TD = (BLK / NW + 1 < TPW) ? BLK / NW + 1 : TPW;
 #pragma unroll
-          for (int t = 0; t < TPW; ++t) {
+          for (int t = 0; t < TD; ++t) {
             float* acc = g + 2 * (t & 1);
-            if (NW * t <= BLK) {
-              const int rb = 16 * (wave + NW * t) + 4 * kq;
-              f32x4 y;
+            const int rb = 16 * (wave + NW * t) + 4 * kq;
+            f32x4 y;
 #pragma unroll
-              for (int i = 0; i < 4; ++i) y[i] = (rb + i > JG) ? X[BLK][t][i] : 0.0f;
-              bcast_dot4<JJ>(acc[0], acc[1], X[BLK][t], y);
-            } else {
-              bcast_dot4<JJ>(acc[0], acc[1], X[BLK][t], X[BLK][t]);
-            }
+            for (int i = 0; i < 4; ++i) y[i] = (rb + i > JG) ? X[BLK][t][i] : 0.0f;
+            bcast_dot4<JJ>(acc[0], acc[1], X[BLK][t], y);
           }
+#pragma unroll
+          for (int t = TD; t + 1 < TPW; t += 2)
+            bcast_dot8<JJ>(g[0], g[1], g[2], g[3], X[BLK][t], X[BLK][t], X[BLK][t + 1], X[BLK][t + 1]);
+          if constexpr (((TPW - TD) & 1) != 0) bcast_dot4<JJ>(g[0], g[1], X[BLK][TPW - 1], X[BLK][TPW - 1]);
           float tot = (g[0] + g[1]) + (g[2] + g[3]);
           // row JG of my column: tile T_OWN of wave W_OWN, register JJ % 4 of lane row JJ / 4
           const bool row_owner = (wave == W_OWN) && (kq == JJ / 4);
@@ -210,15 +251,14 @@ __device__ __forceinline__ void panel_body(IO& io, int m, int tid) {
           const float s = (cn > JJ) ? rf.tau * z : 0.0f;
           const float alp = -s * rf.inv;
 #pragma unroll
-          for (int t = 0; t < TPW; ++t) {
-            if (NW * t <= BLK) {
-              const int rb = 16 * (wave + NW * t) + 4 * kq;
-              bcast_axpy4<JJ>(X[BLK][t], (rb > JG) ? alp : 0.0f, (rb + 1 > JG) ? alp : 0.0f,
-                              (rb + 2 > JG) ? alp : 0.0f, (rb + 3 > JG) ? alp : 0.0f);
-            } else {
-              bcast_axpy4<JJ>(X[BLK][t], alp, alp, alp, alp);
-            }
+          for (int t = 0; t < TD; ++t) {
+            const int rb = 16 * (wave + NW * t) + 4 * kq;
+            bcast_axpy4<JJ>(X[BLK][t], (rb > JG) ? alp : 0.0f, (rb + 1 > JG) ? alp : 0.0f,
+                            (rb + 2 > JG) ? alp : 0.0f, (rb + 3 > JG) ? alp : 0.0f);
           }
+#pragma unroll
+          for (int t = TD; t + 1 < TPW; t += 2) bcast_axpy8<JJ>(X[BLK][t], X[BLK][t + 1], alp);
+          if constexpr (((TPW - TD) & 1) != 0) bcast_axpy4<JJ>(X[BLK][TPW - 1], alp, alp, alp, alp);
           {
             const float a = X[BLK][T_OWN][JJ & 3];
             const float nv = (cn == JJ) ? rf.beta : a - s;
