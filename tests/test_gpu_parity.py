@@ -88,6 +88,21 @@ def test_tall_matrices_match_geqrf(cuda, batch, n):
     _say(f"  {ag.message()}")
 
 
+@pytest.mark.parametrize("batch,n", [(16, 1088), (17, 1100), (7, 1999), (5, 385), (33, 400)])
+def test_scheduling_variants_match_geqrf(cuda, batch, n):
+    # small batches of tall matrices (batch <= 16, n > 1024) run the narrow
+    # updates after 32-column panels on the row-split kernels, batch 17 on the
+    # strip-resident ones; n = 385 and 400: three panel groups, so the wide
+    # update is split (the next look-ahead's columns first) and T slots
+    # rotate over three banks
+    _say(f"[sched] batch={batch} n={n}")
+    a = gaussian(batch, n, 700 + n + batch)
+    h, tau = run_gpu(a, cuda)
+    assert h.stride() == (n * n, 1, n)
+    ag = assert_parity(a, h, tau)
+    _say(f"  {ag.message()}")
+
+
 @pytest.mark.parametrize("n", [32, 176, 512])
 def test_upper_triangular_input_is_left_unchanged(cuda, n):
     # known answer from the reference's tests (tests/test_qr_smoke.py:8078-8085):
