@@ -318,6 +318,57 @@ size_t fastqr_workspace_bytes(int64_t batch, int64_t n) {
   return (floats * sizeof(float) + 255) & ~(size_t)255;
 }
 
+size_t fastqr_orgqr_workspace_bytes(int64_t batch, int64_t n) {
+  if (batch <= 0 || n <= 0 || n > kMaxN) return 0;
+  return (fastqr::orgqr_workspace_floats(batch, (int)n) * sizeof(float) + 255) & ~(size_t)255;
+}
+
+int fastqr_orgqr_f32(const float* H, int64_t batch, int64_t n, int64_t h_s0, int64_t h_s1, int64_t h_s2,
+                     const float* tau, int64_t tau_s0, int64_t tau_s1, float* Q, int64_t q_s0, int64_t q_s1,
+                     int64_t q_s2, void* workspace, size_t workspace_bytes, void* stream_ptr) {
+  g_last_error[0] = '\0';
+  if (g_forced_error != 0) {
+    const int code = g_forced_error;
+    g_forced_error = 0;
+    return fail(code, "forced error %d (test hook)", code);
+  }
+  if (batch < 0 || n < 0) return fail(FASTQR_EINVAL, "batch and n must be non-negative (got %lld, %lld)",
+                                      (long long)batch, (long long)n);
+  if (batch == 0 || n == 0) return FASTQR_OK;
+  if (n > kMaxN) return fail(FASTQR_EINVAL, "n=%lld exceeds the supported maximum %lld", (long long)n,
+                             (long long)kMaxN);
+  if (batch > 65535) return fail(FASTQR_EINVAL, "batch %lld exceeds 65535", (long long)batch);
+  if (!H || !tau || !Q) return fail(FASTQR_EINVAL, "H, tau and Q must be non-null device pointers");
+  if (h_s0 < 0 || h_s1 < 0 || h_s2 < 0 || q_s0 < 0 || q_s2 < 0 || tau_s0 < 0 || tau_s1 < 0)
+    return fail(FASTQR_EINVAL, "negative strides are not supported");
+  if (batch > 1 && (q_s0 == 0 || tau_s0 == 0))
+    return fail(FASTQR_EINVAL, "Q and tau batch strides must be non-zero when batch > 1");
+  if (n > 1 && (tau_s1 == 0 || h_s1 == 0 || h_s2 == 0)) return fail(FASTQR_EINVAL, "H and tau strides must be non-zero");
+  if (q_s1 != 1 || q_s2 < n)
+    return fail(FASTQR_ELAYOUT, "Q must have contiguous columns (stride (*, 1, >=n)); got (%lld, %lld, %lld)",
+                (long long)q_s0, (long long)q_s1, (long long)q_s2);
+  if (q_s2 * n * 4 >= (int64_t)1 << 31)
+    return fail(FASTQR_ELAYOUT, "one matrix of Q spans %lld bytes; at most 2 GiB are addressed",
+                (long long)(q_s2 * n * 4));
+  if (batch > 1 && q_s0 < q_s2 * n)
+    return fail(FASTQR_ELAYOUT, "Q batch stride %lld smaller than one matrix (%lld)", (long long)q_s0,
+                (long long)(q_s2 * n));
+  const size_t need = fastqr_orgqr_workspace_bytes(batch, n);
+  if (workspace_bytes < need || workspace == nullptr)
+    return fail(FASTQR_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+  if (((uintptr_t)workspace & 15) != 0) return fail(FASTQR_EWORKSPACE, "workspace must be 16-byte aligned");
+  const bool same = ((const float*)Q == H && q_s0 == h_s0 && q_s1 == h_s1 && q_s2 == h_s2);
+  const int64_t q_span = span_elems(batch, n, q_s0, 1, q_s2);
+  if (!same && ranges_overlap(H, span_elems(batch, n, h_s0, h_s1, h_s2), Q, q_span))
+    return fail(FASTQR_EOVERLAP, "H and Q overlap with different layouts");
+  if (ranges_overlap(tau, span_elems(batch, n, tau_s0, tau_s1, 0), Q, q_span))
+    return fail(FASTQR_EOVERLAP, "tau and Q overlap");
+  const bool vec = ((uintptr_t)Q % 16 == 0) && (q_s0 % 4 == 0) && (q_s2 % 4 == 0) && (n % 4 == 0);
+  const hipError_t e = fastqr::launch_orgqr(H, batch, (int)n, h_s0, h_s1, h_s2, tau, tau_s0, tau_s1, Q, q_s0, q_s2,
+                                            (float*)workspace, vec, (hipStream_t)stream_ptr);
+  return e == hipSuccess ? FASTQR_OK : hip_fail(e, "orgqr launch");
+}
+
 int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a_s1, int64_t a_s2,
                      float* H, int64_t h_s0, int64_t h_s1, int64_t h_s2, float* tau, int64_t tau_s0,
                      int64_t tau_s1, void* workspace, size_t workspace_bytes, void* stream_ptr) {

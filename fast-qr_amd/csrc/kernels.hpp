@@ -82,4 +82,13 @@ constexpr int kMaxWY = 4;
 // two groups before it are still being applied.
 constexpr int kMaxSlots = 3 * kMaxWY;
 
+// Explicit Q from (H, tau) (qr_orgqr.hip): backward accumulation over
+// 32-column panels in place in Q.  Above kOrgqrRowSplitMinN rows the panel
+// updates run on the row-split kernels.
+constexpr int kOrgqrRowSplitMinN = 2048;
+size_t orgqr_workspace_floats(int64_t batch, int n);
+hipError_t launch_orgqr(const float* H, int64_t batch, int n, int64_t hs0, int64_t hs1, int64_t hs2, const float* tau,
+                        int64_t ts0, int64_t ts1, float* Q, int64_t qs0, int64_t ldq, float* ws, bool vec,
+                        hipStream_t stream);
+
 }  // namespace fastqr

@@ -27,6 +27,8 @@ FASTQR_ETESTHOOK = -99
 EXPORTED_SYMBOLS = (
     "fastqr_geqrf_f32",
     "fastqr_workspace_bytes",
+    "fastqr_orgqr_f32",
+    "fastqr_orgqr_workspace_bytes",
     "fastqr_path_name",
     "fastqr_last_error",
     "fastqr_version",
@@ -71,6 +73,10 @@ def cdll() -> ctypes.CDLL:
         lib.fastqr_geqrf_f32.argtypes = [vp, i64, i64, i64, i64, i64, vp, i64, i64, i64, vp, i64, i64, vp, sz, vp]
         lib.fastqr_geqrf_f32.restype = ctypes.c_int
         lib.fastqr_workspace_bytes.argtypes = [i64, i64]
+        lib.fastqr_orgqr_f32.argtypes = [vp, i64, i64, i64, i64, i64, vp, i64, i64, vp, i64, i64, i64, vp, sz, vp]
+        lib.fastqr_orgqr_f32.restype = ctypes.c_int
+        lib.fastqr_orgqr_workspace_bytes.argtypes = [i64, i64]
+        lib.fastqr_orgqr_workspace_bytes.restype = sz
         lib.fastqr_workspace_bytes.restype = sz
         lib.fastqr_path_name.argtypes = [i64]
         lib.fastqr_path_name.restype = ctypes.c_char_p

@@ -80,6 +80,39 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n,
 size_t fastqr_workspace_bytes(int64_t batch, int64_t n);
 
 /*
+ * Explicit Q of batched compact-Householder factors: Q = H_0 H_1 ... H_{n-1}
+ * with H_k = I - tau[k] v_k v_k^T, v_k below the diagonal of column k of H
+ * (implicit unit at row k).  Replaces torch.linalg.householder_product(H, tau),
+ * the reference checker's call (official/reference.py:199), for square H and
+ * n reflectors.
+ *
+ * H      device pointer, element (b, i, j) at H[b*h_s0 + i*h_s1 + j*h_s2]
+ *        (any strides, read only; only the strictly lower part is read).
+ * tau    device pointer, element (b, k) at tau[b*tau_s0 + k*tau_s1].
+ * Q      device pointer, element (b, i, j) at Q[b*q_s0 + i*q_s1 + j*q_s2];
+ *        columns contiguous (q_s1 == 1, q_s2 >= n).  Q may be H itself with
+ *        the identical layout (formed in place, as LAPACK sorgqr); otherwise
+ *        the two must not overlap.
+ * workspace / workspace_bytes  at least fastqr_orgqr_workspace_bytes(batch, n)
+ *        bytes of device scratch, 16-byte aligned (T and T V1^T per 32-column
+ *        panel; for n > 2048 also the row-split partial products).
+ * stream a hipStream_t; asynchronous, no host synchronisation.
+ *
+ * Returns FASTQR_OK, a negative FASTQR_E* argument error, or a positive
+ * hipError_t if a launch failed.
+ */
+int fastqr_orgqr_f32(const float* H, int64_t batch, int64_t n,
+                     int64_t h_s0, int64_t h_s1, int64_t h_s2,
+                     const float* tau, int64_t tau_s0, int64_t tau_s1,
+                     float* Q, int64_t q_s0, int64_t q_s1, int64_t q_s2,
+                     void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* Workspace bytes fastqr_orgqr_f32 needs for (batch, n).  The reference's
+ * householder_product call allocates its own (official/reference.py:199). */
+size_t fastqr_orgqr_workspace_bytes(int64_t batch, int64_t n);
+
+/*
  * Name of the kernel path fastqr_geqrf_f32 takes for size n ("wave64",
  * "lds", "blocked"); the reference's shape switch is custom_kernel
  * (submissions/candidate.py:8383-8415).  Never NULL.

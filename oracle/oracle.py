@@ -151,6 +151,30 @@ def larft(v: np.ndarray, tau: np.ndarray) -> np.ndarray:
     return np.ascontiguousarray(t)
 
 
+def orgqr_restated(h, tau, mutation: int = 0) -> np.ndarray:
+    """Q = H_0 H_1 ... H_{n-1} from compact factors, in fp64 (numpy).
+
+    The product torch.linalg.householder_product forms for the reference's
+    checker (official/reference.py:199): reflectors applied to I from the
+    last to the first (LAPACK sorg2r's order), v_k = (0, .., 0, 1, h[k+1:, k]).
+    ``mutation`` plants a mistake for the tests: 1 applies them first to last
+    (giving Q^T).
+    """
+    h = np.asarray(h, dtype=np.float64)
+    tau = np.asarray(tau, dtype=np.float64)
+    single = h.ndim == 2
+    if single:
+        h, tau = h[None], tau[None]
+    b, n, _ = h.shape
+    q = np.broadcast_to(np.eye(n), (b, n, n)).copy()
+    order = range(n) if mutation == 1 else range(n - 1, -1, -1)
+    for k in order:
+        v = np.concatenate([np.ones((b, 1)), h[:, k + 1:, k]], axis=1)  # (b, n - k)
+        w = np.einsum("bi,bij->bj", v, q[:, k:, :])
+        q[:, k:, :] -= tau[:, k, None, None] * v[:, :, None] * w[:, None, :]
+    return q[0] if single else q
+
+
 def geqrf_lapack(a):
     """The reference's own path: batched torch.geqrf on CPU (fp32, MKL LAPACK)."""
     import torch

@@ -209,3 +209,48 @@ def test_bench_refuses_multi_gpu():
                        env=env, timeout=120)
     assert r.returncode == 2
     assert "one GPU" in r.stderr
+
+
+def _orgqr_call(lib, H=8, b=2, n=100, h_s=None, tau=32, t_s=None, Q=16, q_s=None, ws=64, ws_bytes=1 << 30):
+    h_s0, h_s1, h_s2 = (n * n, 1, n) if h_s is None else h_s
+    q_s0, q_s1, q_s2 = (n * n, 1, n) if q_s is None else q_s
+    t_s0, t_s1 = (n, 1) if t_s is None else t_s
+    base = 1 << 40  # fake, never-dereferenced addresses (validation only)
+    return lib.fastqr_orgqr_f32(base * H if H else None, b, n, h_s0, h_s1, h_s2, base * tau if tau else None,
+                                t_s0, t_s1, base * Q if Q else None, q_s0, q_s1, q_s2, base * ws if ws else None,
+                                ws_bytes, None)
+
+
+def test_orgqr_argument_validation_returns_codes_without_launching():
+    lib = fastqr.cdll()
+    assert lib.fastqr_orgqr_workspace_bytes(0, 64) == 0
+    one = lib.fastqr_orgqr_workspace_bytes(1, 512)
+    assert one > 0 and one % 256 == 0
+    assert lib.fastqr_orgqr_workspace_bytes(640, 512) >= 640 * one - 255
+    assert _orgqr_call(lib, b=0) == _lib.FASTQR_OK
+    assert _orgqr_call(lib, n=0) == _lib.FASTQR_OK
+    assert _orgqr_call(lib, n=-1) == _lib.FASTQR_EINVAL
+    assert _orgqr_call(lib, n=5000) == _lib.FASTQR_EINVAL
+    assert _orgqr_call(lib, Q=0) == _lib.FASTQR_EINVAL
+    assert b"non-null" in lib.fastqr_last_error()
+    assert _orgqr_call(lib, q_s=(10000, 100, 1)) == _lib.FASTQR_ELAYOUT
+    assert b"contiguous columns" in lib.fastqr_last_error()
+    assert _orgqr_call(lib, ws_bytes=16) == _lib.FASTQR_EWORKSPACE
+    assert _orgqr_call(lib, ws=0) == _lib.FASTQR_EWORKSPACE
+    # H and Q overlapping with different layouts; tau inside Q
+    assert _orgqr_call(lib, H=16, h_s=(10000, 100, 1)) == _lib.FASTQR_EOVERLAP
+    assert _orgqr_call(lib, tau=16) == _lib.FASTQR_EOVERLAP
+    lib.fastqr_debug_force_error(-99)
+    assert _orgqr_call(lib) == -99
+
+
+def test_householder_product_rejects_bad_inputs_loudly():
+    h = torch.zeros((2, 8, 8))
+    with pytest.raises(ValueError):
+        fastqr.householder_product(h, torch.zeros((2, 8)))  # CPU tensors
+    with pytest.raises(TypeError):
+        fastqr.householder_product(h.double(), torch.zeros((2, 8)))
+    with pytest.raises(ValueError):
+        fastqr.householder_product(torch.zeros((2, 8, 7)), torch.zeros((2, 8)))
+    with pytest.raises(ValueError):
+        fastqr.householder_product(h, torch.zeros((2, 7)))
