@@ -40,6 +40,7 @@ for _p in (str(ROOT), str(ROOT / "fast-qr_amd")):
         sys.path.insert(0, _p)
 
 METRIC = "geomean µs/call over 5 configs; GFLOP/s (4n³/3) and % fp32 peak per shape"
+METRIC_OFFICIAL = "geomean µs/call over the task's 12 benchmark cases"
 PEAK_FP32_TFLOPS = 157.3  # MI355X dense fp32 (vector and MFMA)
 PEAK_HBM_GBS = 8000.0
 FLUSH_BYTES = 1 << 30
@@ -61,6 +62,11 @@ def parse_args():
                    help="target CPU seconds per shape for the torch.geqrf baseline (0 disables)")
     p.add_argument("--no-check", action="store_true", help="skip the post-timing recheck")
     p.add_argument("--no-profile", action="store_true", help="skip the instrumented per-kernel pass")
+    p.add_argument("--no-orgqr", action="store_true",
+                   help="skip timing householder_product (explicit Q from the factors) per shape")
+    p.add_argument("--official", action="store_true",
+                   help="time the task's own 12 benchmark cases (official/task.yml) instead of the five workloads; "
+                        "value = geomean over the 12 cases")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="start with a plain 256 MiB device copy (the reference kernel for HBM counter scaling)")
     p.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -177,7 +183,7 @@ def main() -> int:
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world > 1:
         log("bench.py measures one GPU only: every matrix is independent, so the path shards by batch "
-            "with no communication (see DESIGN.md); run with --gpus 1.")
+            "with no communication; run with --gpus 1.")
         return 2
 
     import torch
@@ -201,8 +207,24 @@ def main() -> int:
         torch.cuda.synchronize()
         del src, dst
 
-    names = [c.strip() for c in args.configs.split(",") if c.strip()]
-    shapes = [(name, s) for name in names for s in inputs.WORKLOADS[name]]
+    # groups: name -> shapes; the headline is the geomean over groups of the
+    # geomean over a group's shapes
+    if args.official:
+        from dataclasses import replace
+
+        from fastqr import cases
+
+        groups = {f"B{i + 1:02d}": (c,) for i, c in enumerate(cases.BENCHMARKS)}
+
+        def make_input(s, i):
+            return cases.generate(replace(s, seed=s.seed + 42 * i))
+    else:
+        groups = {name.strip(): inputs.WORKLOADS[name.strip()] for name in args.configs.split(",") if name.strip()}
+
+        def make_input(s, i):
+            return inputs.generate(s, seed=s.seed + 42 * (i + 1))
+    names = list(groups)
+    shapes = [(name, s) for name in names for s in groups[name]]
 
     # ---- inputs -----------------------------------------------------------
     data = {}
@@ -211,8 +233,7 @@ def main() -> int:
         cnt = count_for(s.batch, s.n)
         lst = []
         for i in range(cnt):
-            a = inputs.generate(s, seed=s.seed + 42 * (i + 1))
-            lst.append(a.to(dev))
+            lst.append(make_input(s, i).to(dev))
         data[s.label] = lst
         log(f"[inputs] {name} {s.label}: {cnt} x {tuple(lst[0].shape)}")
     log(f"[inputs] generated in {time.time() - t0:.1f}s")
@@ -273,6 +294,28 @@ def main() -> int:
             kernels[s.label] = _lib.profile_collect()
             _lib.profile_enable(False)
 
+    # ---- explicit Q: householder_product on each timed input's factors --------------
+    # (the reference checker's consumer of (H, tau), official/reference.py:199)
+    orgqr_us = {}
+    if not args.no_orgqr:
+        for _, s in shapes:
+            facs = run_shape(s.label)
+            fastqr.householder_product(*facs[0])  # warm
+            torch.cuda.synchronize()
+            times = []
+            for _ in range(max(1, args.steps)):
+                flush_buf.fill_(42)
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for h, tau in facs:
+                    fastqr.householder_product(h, tau)
+                e1.record()
+                torch.cuda.synchronize()
+                times.append(e0.elapsed_time(e1) * 1e3 / len(facs))
+            orgqr_us[s.label] = statistics.median(times)
+            del facs
+
     # ---- CPU baseline: torch.geqrf on this host's cores ------------------------
     cpu = {}
     if args.cpu_sample_seconds > 0:
@@ -294,6 +337,12 @@ def main() -> int:
             us_full = statistics.median(reps) * s.batch / k
             cpu[s.label] = {"us_per_call": us_full, "sample_batch": k}
             log(f"[cpu] {s.label}: torch.geqrf {us_full:.1f} us/call (sample {k}/{s.batch}, {ncores} threads)")
+            if s.label in orgqr_us:
+                h_c, t_c = torch.geqrf(sample)
+                torch.linalg.householder_product(h_c, t_c)  # warm
+                t = time.perf_counter_ns()
+                torch.linalg.householder_product(h_c, t_c)
+                cpu[s.label]["orgqr_us"] = (time.perf_counter_ns() - t) / 1e3 * s.batch / k
 
     # ---- report ---------------------------------------------------------------------
     shape_rows = {}
@@ -301,7 +350,7 @@ def main() -> int:
     cfg_cpu = {}
     for name in names:
         us_list, cpu_list = [], []
-        for s in inputs.WORKLOADS[name]:
+        for s in groups[name]:
             us = statistics.median(per_shape_us[s.label])
             best = min(per_shape_us[s.label])
             fl = inputs.flops(s.batch, s.n)
@@ -338,6 +387,17 @@ def main() -> int:
                     if uk in kk and kk[uk]["tflops"] is not None:
                         kk[uk]["pct_fp32_mfma_peak"] = round(100 * kk[uk]["tflops"] / PEAK_FP32_TFLOPS, 2)
                 row["kernels"] = kk
+            if s.label in orgqr_us:
+                qu = orgqr_us[s.label]
+                row["householder_product"] = {
+                    "us_per_call": round(qu, 3),
+                    "gflops": round(fl / (qu * 1e-6) / 1e9, 2),
+                    "pct_fp32_peak": round(100.0 * fl / (qu * 1e-6) / (PEAK_FP32_TFLOPS * 1e12), 2),
+                }
+                if "orgqr_us" in cpu.get(s.label, {}):
+                    row["householder_product"]["cpu_us"] = round(cpu[s.label]["orgqr_us"], 1)
+                log(f"[gpu] {s.label}: householder_product {qu:9.1f} us/call "
+                    f"{row['householder_product']['gflops']:9.1f} GFLOP/s")
             if s.label in cpu:
                 row["cpu_geqrf_us"] = round(cpu[s.label]["us_per_call"], 1)
                 row["speedup_vs_cpu"] = round(cpu[s.label]["us_per_call"] / us, 1)
@@ -385,7 +445,7 @@ def main() -> int:
             }
 
     line = {
-        "metric": METRIC,
+        "metric": METRIC_OFFICIAL if args.official else METRIC,
         "value": round(value, 3),
         "unit": "us/call (geomean over configs)",
         "n_gpus": 1,
@@ -396,11 +456,17 @@ def main() -> int:
         "scaling": "strong",
         "vs_baseline": None,
         "dtype": "f32",
-        "data": "synthetic: seeded N(0,1) and U diag(s) V^T (Haar U, V) families, generated on the CPU",
+        "data": ("synthetic: the task's input profiles (dense, mixed, rankdef, clustered, nearrank), restated, "
+                 "generated on the CPU" if args.official else
+                 "synthetic: seeded N(0,1) and U diag(s) V^T (Haar U, V) families, generated on the CPU"),
         "config": {
-            "workload": "batched fp32 geqrf, configs " + ",".join(names) + " (C2, C5 = geomean of two shapes)",
+            "workload": ("batched fp32 geqrf, the 12 benchmark cases of the task (official/task.yml), "
+                         "geomean over cases" if args.official else
+                         "batched fp32 geqrf, configs " + ",".join(names) + " (C2, C5 = geomean of two shapes)"),
             "config_us": {k: round(v, 3) for k, v in cfg_us.items()},
             "geomean_shapes_us": round(geomean([r["us_per_call"] for r in shape_rows.values()]), 3),
+            "householder_product_geomean_shapes_us": (round(geomean(list(orgqr_us.values())), 3)
+                                                      if orgqr_us else None),
             "shapes": shape_rows,
         },
         "roofline": roof,
