@@ -72,6 +72,9 @@ def parse_args():
     p.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="print the HBM traffic summary of two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
                         "this script with --calibrate-copy, and exit")
+    p.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
+                   help="print per-kernel statistics of a rocprofv3 --kernel-trace run of this script, split into "
+                        "the geqrf calls and the householder_product calls, and exit")
     p.add_argument("--traffic-file", default=str(ROOT / "profiles" / TRAFFIC_SUMMARY),
                    help="committed traffic summary that fills roofline.traffic")
     return p.parse_args()
@@ -153,6 +156,46 @@ def summarize_traffic(fetch_dir: str, write_dir: str) -> str:
     return "\n".join(lines)
 
 
+# kernels only a geqrf call launches; a householder_product call starts with
+# orgqr_init_kernel and runs on one stream, so every dispatch from there to the
+# next of these belongs to it
+GEQRF_ONLY = ("copy_to_colmajor", "qr_wave_kernel", "qr_lds_kernel", "panel_kernel")
+
+
+def summarize_trace(path: str) -> str:
+    """Markdown: per kernel, calls and average/min/max duration, for the geqrf
+    calls and the householder_product calls of a bench.py kernel trace."""
+    import csv
+
+    rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Dispatch_Id"]))
+    stats = {"geqrf": {}, "householder_product": {}}
+    phase = "geqrf"
+    for r in rows:
+        name = r["Kernel_Name"]
+        if "fastqr::" not in name:
+            continue
+        if "orgqr_" in name:
+            phase = "householder_product"
+        elif any(k in name for k in GEQRF_ONLY):
+            phase = "geqrf"
+        short = name.replace("void ", "").split("(")[0]
+        d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
+        ent = stats[phase].setdefault(short, [0, 0.0, float("inf"), 0.0])
+        ent[0] += 1
+        ent[1] += d
+        ent[2] = min(ent[2], d)
+        ent[3] = max(ent[3], d)
+    lines = []
+    for phase, st in stats.items():
+        tot = sum(e[1] for e in st.values()) or 1.0
+        lines += [f"## {phase} calls", "", "| kernel | calls | avg us | min us | max us | % of phase time |",
+                  "|---|---:|---:|---:|---:|---:|"]
+        for k, e in sorted(st.items(), key=lambda kv: -kv[1][1]):
+            lines.append(f"| `{k}` | {e[0]} | {e[1] / e[0]:.2f} | {e[2]:.2f} | {e[3]:.2f} | {100 * e[1] / tot:.2f} |")
+        lines.append("")
+    return "\n".join(lines)
+
+
 def traffic_per_launch(path: str, kind: str):
     """HBM bytes per launch of `kind` from a committed summary, or None."""
     try:
@@ -179,6 +222,9 @@ def main() -> int:
     args = parse_args()
     if args.summarize_traffic:
         print(summarize_traffic(*args.summarize_traffic))
+        return 0
+    if args.summarize_trace:
+        print(summarize_trace(args.summarize_trace))
         return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world > 1:
