@@ -38,12 +38,13 @@ hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float
                         int64_t ts1, float* Tws, int n, int k0, int nb, int m_cap, int slot, bool vec,
                         hipStream_t stream);
 // Apply nwy compact-WY transforms (panels k0 + i*nb, T slots slot0 + i) to
-// columns [c_begin, c_end), rows [k0, n).  max_cus > 0 caps the grid at that
-// many CUs' worth of resident workgroups (the workgroups then loop over the
-// work), leaving the other CUs to kernels on another stream.
+// columns [c_begin, c_end), rows [k0, n), first to last (last to first with
+// `reverse`).  max_cus > 0 caps the grid at that many CUs' worth of resident
+// workgroups (the workgroups then loop over the work), leaving the other CUs
+// to kernels on another stream.
 hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n,
                             int k0, int nb, int slot0, int nwy, int c_begin, int c_end, bool vec, bool hi_prio,
-                            int max_cus, hipStream_t stream);
+                            int max_cus, hipStream_t stream, bool reverse = false);
 
 // Row-split compact-WY update (qr_update.hip): for tall matrices and small
 // batches the trailing update is split over row blocks as well as column
@@ -86,6 +87,7 @@ constexpr int kMaxSlots = 3 * kMaxWY;
 // 32-column panels in place in Q.  Above kOrgqrRowSplitMinN rows the panel
 // updates run on the row-split kernels.
 constexpr int kOrgqrRowSplitMinN = 2048;
+constexpr int64_t kOrgqrGroupMinBatch = 48;  // panels grouped per update from this batch on
 size_t orgqr_workspace_floats(int64_t batch, int n);
 hipError_t launch_orgqr(const float* H, int64_t batch, int n, int64_t hs0, int64_t hs1, int64_t hs2, const float* tau,
                         int64_t ts0, int64_t ts1, float* Q, int64_t qs0, int64_t ldq, float* ws, bool vec,

@@ -3,7 +3,7 @@
  *
  * It only converts Python ints to the ABI's int64 / pointer arguments
  * (METH_FASTCALL, no argument tuples) and returns the status code; all
- * validation and every launch happen behind fastqr_geqrf_f32.  It exists so
+ * validation and every launch happen behind fastqr_geqrf_f32 / fastqr_orgqr_f32.  It exists so
  * that a call costs well under a microsecond of host time; ctypes over the
  * same library is equivalent and is what the tests use to check the ABI.
  */
@@ -45,6 +45,35 @@ static PyObject* py_geqrf(PyObject* self, PyObject* const* args, Py_ssize_t narg
   return PyLong_FromLong(rc);
 }
 
+/* orgqr(H, batch, n, hs0, hs1, hs2, tau, ts0, ts1, Q, qs0, qs1, qs2, ws, ws_bytes, stream) -> int */
+static PyObject* py_orgqr(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
+  (void)self;
+  if (nargs != 16) {
+    PyErr_SetString(PyExc_TypeError, "orgqr expects 16 integer arguments");
+    return NULL;
+  }
+  void *H, *tau, *Q, *ws, *stream;
+  int64_t b, n, hs0, hs1, hs2, ts0, ts1, qs0, qs1, qs2, wsb;
+  if (as_ptr(args[0], &H) || as_i64(args[1], &b) || as_i64(args[2], &n) || as_i64(args[3], &hs0) ||
+      as_i64(args[4], &hs1) || as_i64(args[5], &hs2) || as_ptr(args[6], &tau) || as_i64(args[7], &ts0) ||
+      as_i64(args[8], &ts1) || as_ptr(args[9], &Q) || as_i64(args[10], &qs0) || as_i64(args[11], &qs1) ||
+      as_i64(args[12], &qs2) || as_ptr(args[13], &ws) || as_i64(args[14], &wsb) || as_ptr(args[15], &stream))
+    return NULL;
+  const int rc = fastqr_orgqr_f32((const float*)H, b, n, hs0, hs1, hs2, (const float*)tau, ts0, ts1, (float*)Q, qs0,
+                                  qs1, qs2, ws, (size_t)wsb, stream);
+  return PyLong_FromLong(rc);
+}
+
+static PyObject* py_orgqr_workspace_bytes(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
+  (void)self;
+  int64_t b, n;
+  if (nargs != 2 || as_i64(args[0], &b) || as_i64(args[1], &n)) {
+    if (!PyErr_Occurred()) PyErr_SetString(PyExc_TypeError, "orgqr_workspace_bytes(batch, n)");
+    return NULL;
+  }
+  return PyLong_FromSize_t(fastqr_orgqr_workspace_bytes(b, n));
+}
+
 static PyObject* py_workspace_bytes(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
   (void)self;
   int64_t b, n;
@@ -77,6 +106,9 @@ static PyObject* py_version(PyObject* self, PyObject* unused) {
 static PyMethodDef methods[] = {
     {"geqrf", (PyCFunction)(void (*)(void))py_geqrf, METH_FASTCALL, "fastqr_geqrf_f32 over raw pointers"},
     {"workspace_bytes", (PyCFunction)(void (*)(void))py_workspace_bytes, METH_FASTCALL, "fastqr_workspace_bytes"},
+    {"orgqr", (PyCFunction)(void (*)(void))py_orgqr, METH_FASTCALL, "fastqr_orgqr_f32 over raw pointers"},
+    {"orgqr_workspace_bytes", (PyCFunction)(void (*)(void))py_orgqr_workspace_bytes, METH_FASTCALL,
+     "fastqr_orgqr_workspace_bytes"},
     {"last_error", py_last_error, METH_NOARGS, "fastqr_last_error"},
     {"path_name", py_path_name, METH_O, "fastqr_path_name"},
     {"version", py_version, METH_NOARGS, "fastqr_version"},

@@ -87,7 +87,8 @@ __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __re
 // ---------------------------------------------------------------------------
 // Trailing update  A2 <- A2 - V T^T V^T A2  (fp32 MFMA 32x32x2)
 // ---------------------------------------------------------------------------
-// Applies `nwy` consecutive compact-WY transforms, transform i starting at
+// Applies `nwy` consecutive compact-WY transforms (last to first when `rev`),
+// transform i starting at
 // row and column kw = k0 + i*nb with width nb (<= 32) and T factor in
 // workspace slot (slot0 + i), to the 32-column strip
 // [c_begin + 32*strip, +32) of [c_begin, c_end), rows [k0, n).  The strip
@@ -100,7 +101,7 @@ __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __re
 template <int NW, int TPW, bool RES, bool VEC>
 __device__ __forceinline__ void wy_update_item(float* __restrict__ H, int64_t hs0, int64_t ldh,
                                                const float* __restrict__ Tws, int n, int k0, int nb, int slot0,
-                                               int nwy, int c_begin, int c_end, int64_t b, int strip) {
+                                               int nwy, int rev, int c_begin, int c_end, int64_t b, int strip) {
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar branches on tiles
   const int h = lane >> 5;
@@ -153,7 +154,9 @@ __device__ __forceinline__ void wy_update_item(float* __restrict__ H, int64_t hs
   }
   __syncthreads();
 
-  for (int i = 0; i < nwy; ++i) {
+  for (int step = 0; step < nwy; ++step) {
+    // rev: last transform first (backward accumulation of Q)
+    const int i = rev ? nwy - 1 - step : step;
     const int kw = k0 + i * nb;
     const int rt_first = (kw - k0) >> 5;  // tiles above this transform are untouched
     // Row base made opaque per transform: the per-tile row indices and offsets
@@ -286,7 +289,7 @@ template <int NW, int TPW, bool RES, bool VEC>
 __global__ void __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu((TPW >= 2 && NW >= 4) || (TPW >= 4 && NW <= 4) ? 2 : 4, 8)))
 wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* __restrict__ Tws, int n, int k0,
-                 int nb, int slot0, int nwy, int c_begin, int c_end, int hi_prio, int nstrips, int batch) {
+                 int nb, int slot0, int nwy, int rev, int c_begin, int c_end, int hi_prio, int nstrips, int batch) {
   // updates on the critical path (the rest of a panel group, the next group's
   // columns) win issue arbitration against the wide update they overlap
   if (hi_prio) __builtin_amdgcn_s_setprio(2);
@@ -295,7 +298,7 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
     const int xk = L >> 3;
     const int64_t b = (L & 7) + 8 * (xk / nstrips);
     const int strip = xk % nstrips;
-    if (b < batch) wy_update_item<NW, TPW, RES, VEC>(H, hs0, ldh, Tws, n, k0, nb, slot0, nwy, c_begin, c_end, b, strip);
+    if (b < batch) wy_update_item<NW, TPW, RES, VEC>(H, hs0, ldh, Tws, n, k0, nb, slot0, nwy, rev, c_begin, c_end, b, strip);
     __syncthreads();  // the next item rewrites the LDS buffers
   }
 }
@@ -335,7 +338,7 @@ int wgs_per_cu(K kernel, int threads) {
 
 hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n,
                             int k0, int nb, int slot0, int nwy, int c_begin, int c_end, bool vec, bool hi_prio,
-                            int max_cus, hipStream_t stream) {
+                            int max_cus, hipStream_t stream, bool reverse) {
   const int cols = c_end - c_begin;
   if (cols <= 0 || nwy <= 0) return hipSuccess;
   const int ntiles = (n - k0 + 31) / 32;
@@ -380,14 +383,15 @@ hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, c
   }
   const bool res = nw * tpw >= ntiles;
   const int prio = hi_prio ? 1 : 0;
+  const int rv = reverse ? 1 : 0;
 #define FASTQR_WY(NW, TPW, RES)                                                                                 \
   if (nw == NW && tpw == TPW && res == RES) {                                                                   \
     if (vec)                                                                                                    \
       hipLaunchKernelGGL((wy_update_kernel<NW, TPW, RES, true>), grid_for(wy_update_kernel<NW, TPW, RES, true>, NW * 64), dim3(NW * 64), 0, stream, H, hs0, ldh,    \
-                         Tws, n, k0, nb, slot0, nwy, c_begin, c_end, prio, ns, nbatch);                                     \
+                         Tws, n, k0, nb, slot0, nwy, rv, c_begin, c_end, prio, ns, nbatch);                                     \
     else                                                                                                        \
       hipLaunchKernelGGL((wy_update_kernel<NW, TPW, RES, false>), grid_for(wy_update_kernel<NW, TPW, RES, false>, NW * 64), dim3(NW * 64), 0, stream, H, hs0, ldh,   \
-                         Tws, n, k0, nb, slot0, nwy, c_begin, c_end, prio, ns, nbatch);                                     \
+                         Tws, n, k0, nb, slot0, nwy, rv, c_begin, c_end, prio, ns, nbatch);                                     \
     return hipGetLastError();                                                                                   \
   }
   FASTQR_WY(1, 1, true)
@@ -407,10 +411,10 @@ hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, c
   // strips taller than 8 waves x 8 tiles: stream the tiles
   if (vec)
     hipLaunchKernelGGL((wy_update_kernel<16, 1, false, true>), grid_for(wy_update_kernel<16, 1, false, true>, 1024), dim3(16 * 64), 0, stream, H, hs0, ldh, Tws, n,
-                       k0, nb, slot0, nwy, c_begin, c_end, prio, ns, nbatch);
+                       k0, nb, slot0, nwy, rv, c_begin, c_end, prio, ns, nbatch);
   else
     hipLaunchKernelGGL((wy_update_kernel<16, 1, false, false>), grid_for(wy_update_kernel<16, 1, false, false>, 1024), dim3(16 * 64), 0, stream, H, hs0, ldh, Tws, n,
-                       k0, nb, slot0, nwy, c_begin, c_end, prio, ns, nbatch);
+                       k0, nb, slot0, nwy, rv, c_begin, c_end, prio, ns, nbatch);
   return hipGetLastError();
 }
 

@@ -34,10 +34,12 @@ __global__ void __launch_bounds__(256) orgqr_init_kernel(const float* __restrict
 }
 
 // T and Y of one 32-column panel.  Rows are staged through LDS 64 at a time
-// (the next chunk's loads in flight while the current one is summed); thread
-// (i, j0) accumulates G(i, j0..j0+3) = sum_r V(r, i) V(r, j0..j0+3).  The
-// slarft recurrence T(i, j) = -tau_j sum_{i <= l < j} T(i, l) G(l, j) needs
-// only row i of T, so lane i runs it alone.
+// (the next chunk's loads in flight while the current one is used); the four
+// waves split each chunk's rows and accumulate G = V^T V with
+// v_mfma_f32_32x32x2f32: for rows (r, r+1) lane (h, c) holds V(r+h, c), which
+// is both its A element (V^T) and its B element (V).  The slarft recurrence
+// T(i, j) = -tau_j sum_{i <= l < j} T(i, l) G(l, j) needs only row i of T, so
+// lane i runs it alone.
 __global__ void __launch_bounds__(256) orgqr_larft_kernel(const float* __restrict__ Q, int64_t qs0, int ldq, int n,
                                                           const float* __restrict__ tau, int64_t ts0, int64_t ts1,
                                                           int64_t batch, float* __restrict__ Tws,
@@ -49,12 +51,14 @@ __global__ void __launch_bounds__(256) orgqr_larft_kernel(const float* __restric
   const int m = n - k0;
   const float* Qb = Q + b * qs0;
   const int t = threadIdx.x;
-  const int gi = t >> 3, gj = 4 * (t & 7);
+  const int lane = t & 63, h = lane >> 5, l32 = lane & 31;
+  const int wave = __builtin_amdgcn_readfirstlane(t >> 6);
 
-  __shared__ __attribute__((aligned(16))) float Vs[64][36];
+  __shared__ float Vs[64][33];
   __shared__ float V1s[32][33];
   __shared__ float Gs[32][33];
   __shared__ float Ts[32][33];
+  __shared__ float Gp[4][16][64];
   __shared__ float taus[32];
   if (t < 32) taus[t] = (t < nb) ? tau[b * ts0 + (int64_t)(k0 + t) * ts1] : 0.0f;
 
@@ -69,7 +73,9 @@ __global__ void __launch_bounds__(256) orgqr_larft_kernel(const float* __restric
       v[u] = x;
     }
   };
-  float acc[4] = {0.0f, 0.0f, 0.0f, 0.0f};
+  f32x16 acc;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) acc[j] = 0.0f;
   float nxt[8];
   fetch(0, nxt);
   for (int r0 = 0; r0 < m; r0 += 64) {
@@ -87,36 +93,42 @@ __global__ void __launch_bounds__(256) orgqr_larft_kernel(const float* __restric
       }
     }
     if (r0 + 64 < m) fetch(r0 + 64, nxt);
-    const int rows = min(64, m - r0);
-    for (int rr = 0; rr < rows; ++rr) {
-      const float a = Vs[rr][gi];
-      const f32x4 w = *reinterpret_cast<const f32x4*>(&Vs[rr][gj]);
-      acc[0] = fmaf(a, w[0], acc[0]);
-      acc[1] = fmaf(a, w[1], acc[1]);
-      acc[2] = fmaf(a, w[2], acc[2]);
-      acc[3] = fmaf(a, w[3], acc[3]);
+    // rows past m were staged as zeros: the whole chunk can be summed
+#pragma unroll
+    for (int k = 0; k < 8; ++k) {
+      const float v = Vs[16 * wave + 2 * k + h][l32];
+      acc = __builtin_amdgcn_mfma_f32_32x32x2f32(v, v, acc, 0, 0, 0);
     }
     __syncthreads();
   }
 #pragma unroll
-  for (int q = 0; q < 4; ++q) Gs[gi][gj + q] = acc[q];
+  for (int j = 0; j < 16; ++j) Gp[wave][j][lane] = acc[j];
+  __syncthreads();
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int e = t + 256 * u;
+    const int j = e >> 6, ln = e & 63;
+    const float g = (Gp[0][j][ln] + Gp[1][j][ln]) + (Gp[2][j][ln] + Gp[3][j][ln]);
+    Gs[8 * (j >> 2) + 4 * (ln >> 5) + (j & 3)][ln & 31] = g;
+  }
   __syncthreads();
 
+  // Row i of T in registers, every loop unrolled: the G loads of a step do not
+  // wait on its FMA chain (T(i, l) = 0 for l < i, so the sum over l < j only
+  // picks up l >= i; G is symmetric, so row j of Gs is column j of G).
   if (t < 32) {
     const int i = t;
+    float trow[32];
+#pragma unroll
     for (int j = 0; j < 32; ++j) {
-      float v = 0.0f;
-      if (j < nb) {
-        if (i == j) {
-          v = taus[j];
-        } else if (i < j) {
-          float s = 0.0f;
-          for (int l = i; l < j; ++l) s = fmaf(Ts[i][l], Gs[l][j], s);
-          v = -taus[j] * s;
-        }
-      }
-      Ts[i][j] = v;
+      float acc_s = 0.0f;
+#pragma unroll
+      for (int l = 0; l < j; ++l) acc_s = fmaf(trow[l], Gs[j][l], acc_s);
+      const float tj = taus[j];  // 0 for j >= nb
+      trow[j] = (i == j) ? tj : (i < j ? -tj * acc_s : 0.0f);
     }
+#pragma unroll
+    for (int j = 0; j < 32; ++j) Ts[i][j] = trow[j];
   }
   __syncthreads();
 
@@ -127,8 +139,11 @@ __global__ void __launch_bounds__(256) orgqr_larft_kernel(const float* __restric
     const int idx = t + 256 * u;
     const int r = idx >> 5, c = idx & 31;
     To[idx] = Ts[c][r];
+    // Y(r, c) = sum_l T(r, l) V1(c, l): T is zero left of its diagonal and V1
+    // (staged with its unit diagonal and zeros) right of its own
     float y = 0.0f;
-    for (int l = r; l <= c; ++l) y = fmaf(Ts[r][l], V1s[c][l], y);  // T upper, V1 unit lower
+#pragma unroll
+    for (int l = 0; l < 32; ++l) y = fmaf(Ts[r][l], V1s[c][l], y);
     Yo[idx] = y;
   }
 }
@@ -156,11 +171,10 @@ __global__ void __launch_bounds__(256) orgqr_panel_kernel(float* __restrict__ Q,
   }
 #pragma unroll
   for (int c = 0; c < 32; ++c) {
-    if (c >= nb) break;
     float s = 0.0f;
 #pragma unroll
     for (int l = 0; l < 32; ++l) s = fmaf(v[l], Ys[l][c], s);
-    Qc[(int64_t)c * ldq] = (c == rr ? 1.0f : 0.0f) - s;
+    if (c < nb) Qc[(int64_t)c * ldq] = (c == rr ? 1.0f : 0.0f) - s;
   }
 }
 
@@ -189,12 +203,19 @@ hipError_t launch_orgqr(const float* H, int64_t batch, int n, int64_t hs0, int64
                      (int)ldq, n, tau, ts0, ts1, batch, Tws, Yws);
   if ((e = hipGetLastError()) != hipSuccess) return e;
 
-  for (int p = npan - 1; p >= 0; --p) {
-    const int k0 = 32 * p;
-    const int c0 = k0 + 32;
-    float* Tchunk = Tws + (int64_t)(p / kMaxSlots) * batch * kMaxSlots * 1024;
-    if (c0 < n) {
-      if (n > kOrgqrRowSplitMinN) {
+  auto panel_q = [&](int p) -> hipError_t {
+    hipLaunchKernelGGL(orgqr_panel_kernel, dim3((unsigned)((n - 32 * p + 255) / 256), (unsigned)batch), dim3(256), 0,
+                       stream, Q, qs0, (int)ldq, n, p, batch, Yws);
+    return hipGetLastError();
+  };
+  auto t_chunk = [&](int p) { return Tws + (int64_t)(p / kMaxSlots) * batch * kMaxSlots * 1024; };
+
+  if (n > kOrgqrRowSplitMinN) {
+    // tall matrices: one panel per row-split update
+    for (int p = npan - 1; p >= 0; --p) {
+      const int k0 = 32 * p;
+      const int c0 = k0 + 32;
+      if (c0 < n) {
         WyrCall wc{};
         wc.H = Q;
         wc.hs0 = qs0;
@@ -205,21 +226,47 @@ hipError_t launch_orgqr(const float* H, int64_t batch, int n, int64_t hs0, int64
         wc.k = 32;
         wc.c_begin = c0;
         wc.c_end = n;
-        wc.Tws = Tchunk;
-        wc.Tslot = Tchunk + (p % kMaxSlots) * 1024;
+        wc.Tws = t_chunk(p);
+        wc.Tslot = t_chunk(p) + (p % kMaxSlots) * 1024;
         wc.scratch = scratch;
         wc.rows_per_blk = wyr_rows_per_block(n - k0, batch, n - c0);
         wc.vec = vec;
         wc.hi_prio = true;
-        e = launch_wyr(wc, stream);
-      } else {
-        e = launch_wy_update(Q, batch, qs0, ldq, Tchunk, n, k0, 32, p % kMaxSlots, 1, c0, n, vec, false, 0, stream);
+        if ((e = launch_wyr(wc, stream)) != hipSuccess) return e;
       }
+      if ((e = panel_q(p)) != hipSuccess) return e;
+    }
+    return hipSuccess;
+  }
+
+  // Groups of kMaxWY panels (the T chunks hold a whole number of groups).
+  // The group's transforms reach the columns right of it in one update, last
+  // panel first; inside the group, panel p's own columns are formed after its
+  // transform has been applied to the group's columns right of p.  The group
+  // costs kMaxWY - 1 more (narrow) launches than one update per panel and
+  // saves re-reading the trailing matrix: it pays for large batches (measured
+  // on MI355X: 640 x 512 17% and 60 x 1024 24% faster, 8 x 2048 and 40 x 352
+  // 4-6% slower), so small batches keep one update per panel.
+  static_assert(kMaxSlots % kMaxWY == 0, "a panel group must not straddle two T chunks");
+  const int gw = batch >= kOrgqrGroupMinBatch ? kMaxWY : 1;
+  const int ngroups = (npan + gw - 1) / gw;
+  for (int g = ngroups - 1; g >= 0; --g) {
+    const int p0 = gw * g;
+    const int p1 = min(p0 + gw, npan);
+    const int g_end = min(32 * p1, n);
+    if (g_end < n) {
+      e = launch_wy_update(Q, batch, qs0, ldq, t_chunk(p0), n, 32 * p0, 32, p0 % kMaxSlots, p1 - p0, g_end, n, vec,
+                           false, 0, stream, /*reverse=*/true);
       if (e != hipSuccess) return e;
     }
-    hipLaunchKernelGGL(orgqr_panel_kernel, dim3((unsigned)((n - k0 + 255) / 256), (unsigned)batch), dim3(256), 0,
-                       stream, Q, qs0, (int)ldq, n, p, batch, Yws);
-    if ((e = hipGetLastError()) != hipSuccess) return e;
+    for (int p = p1 - 1; p >= p0; --p) {
+      if (32 * p + 32 < g_end) {
+        e = launch_wy_update(Q, batch, qs0, ldq, t_chunk(p), n, 32 * p, 32, p % kMaxSlots, 1, 32 * p + 32, g_end, vec,
+                             false, 0, stream);
+        if (e != hipSuccess) return e;
+      }
+      if ((e = panel_q(p)) != hipSuccess) return e;
+    }
   }
   return hipSuccess;
 }

@@ -10,12 +10,10 @@ a failed call ``FastQRError``).
 """
 from __future__ import annotations
 
-import ctypes
-
 import torch
 
 from . import workspace
-from ._lib import FastQRError, cdll
+from ._lib import FastQRError, ext
 from .qr import _current_stream_ptr
 
 
@@ -51,14 +49,14 @@ def householder_product(h: torch.Tensor, tau: torch.Tensor, *, out: torch.Tensor
         raise ValueError("out must be a float32 (batch, n, n) tensor on h's device")
     if b == 0 or n == 0:
         return out
-    lib = cdll()
+    mod = ext()
     sptr = _current_stream_ptr(idx)
-    nbytes = lib.fastqr_orgqr_workspace_bytes(b, n)
-    ws = workspace.scratch(h.device, sptr, nbytes)
-    rc = lib.fastqr_orgqr_f32(
-        h.data_ptr(), b, n, *h.stride(), tau.data_ptr(), *tau.stride(),
-        out.data_ptr(), *out.stride(), ctypes.c_void_p(ws.data_ptr()), ws.numel(), ctypes.c_void_p(sptr),
-    )
+    ws = workspace.scratch(h.device, sptr, mod.orgqr_workspace_bytes(b, n))
+    hs0, hs1, hs2 = h.stride()
+    ts0, ts1 = tau.stride()
+    qs0, qs1, qs2 = out.stride()
+    rc = mod.orgqr(h.data_ptr(), b, n, hs0, hs1, hs2, tau.data_ptr(), ts0, ts1, out.data_ptr(), qs0, qs1, qs2,
+                   ws.data_ptr(), ws.numel(), sptr)
     if rc != 0:
-        raise FastQRError(rc, lib.fastqr_last_error().decode())
+        raise FastQRError(rc, mod.last_error())
     return out
