@@ -178,11 +178,15 @@ __global__ void __launch_bounds__(256) orgqr_panel_kernel(float* __restrict__ Q,
   }
 }
 
+// Small batches of tall matrices: the narrow updates inside a panel group run
+// on the row-split kernels, spread over row blocks (as geqrf's narrow updates).
+static bool orgqr_narrow_rowsplit(int64_t batch, int n) { return batch <= 16 && n > 1024; }
+
 size_t orgqr_workspace_floats(int64_t batch, int n) {
   const int64_t npan = (n + 31) / 32;
   const int64_t nchunk = (npan + kMaxSlots - 1) / kMaxSlots;
   size_t f = 2 * (size_t)(nchunk * batch * kMaxSlots * 1024);
-  if (n > kOrgqrRowSplitMinN) f += wyr_workspace_floats(batch, n);
+  if (n > kOrgqrRowSplitMinN || orgqr_narrow_rowsplit(batch, n)) f += wyr_workspace_floats(batch, n);
   return f;
 }
 
@@ -246,9 +250,12 @@ hipError_t launch_orgqr(const float* H, int64_t batch, int n, int64_t hs0, int64
   // costs kMaxWY - 1 more (narrow) launches than one update per panel and
   // saves re-reading the trailing matrix: it pays for large batches (measured
   // on MI355X: 640 x 512 17% and 60 x 1024 24% faster, 8 x 2048 and 40 x 352
-  // 4-6% slower), so small batches keep one update per panel.
+  // 4-6% slower), so small batches keep one update per panel -- except tall
+  // matrices in small batches, grouped with their narrow updates on the
+  // row-split kernels (8 x 2048: 3.46 ms per panel, 3.45 ms grouped).
   static_assert(kMaxSlots % kMaxWY == 0, "a panel group must not straddle two T chunks");
-  const int gw = batch >= kOrgqrGroupMinBatch ? kMaxWY : 1;
+  const bool narrow_rs = orgqr_narrow_rowsplit(batch, n);
+  const int gw = (batch >= kOrgqrGroupMinBatch || narrow_rs) ? kMaxWY : 1;
   const int ngroups = (npan + gw - 1) / gw;
   for (int g = ngroups - 1; g >= 0; --g) {
     const int p0 = gw * g;
@@ -261,8 +268,28 @@ hipError_t launch_orgqr(const float* H, int64_t batch, int n, int64_t hs0, int64
     }
     for (int p = p1 - 1; p >= p0; --p) {
       if (32 * p + 32 < g_end) {
-        e = launch_wy_update(Q, batch, qs0, ldq, t_chunk(p), n, 32 * p, 32, p % kMaxSlots, 1, 32 * p + 32, g_end, vec,
-                             false, 0, stream);
+        if (narrow_rs) {
+          WyrCall wc{};
+          wc.H = Q;
+          wc.hs0 = qs0;
+          wc.ldh = (int)ldq;
+          wc.n = n;
+          wc.batch = batch;
+          wc.kv = 32 * p;
+          wc.k = 32;
+          wc.c_begin = 32 * p + 32;
+          wc.c_end = g_end;
+          wc.Tws = t_chunk(p);
+          wc.Tslot = t_chunk(p) + (p % kMaxSlots) * 1024;
+          wc.scratch = scratch;
+          wc.rows_per_blk = wyr_rows_per_block(n - 32 * p, batch, g_end - 32 * p - 32);
+          wc.vec = vec;
+          wc.hi_prio = true;
+          e = launch_wyr(wc, stream);
+        } else {
+          e = launch_wy_update(Q, batch, qs0, ldq, t_chunk(p), n, 32 * p, 32, p % kMaxSlots, 1, 32 * p + 32, g_end,
+                               vec, false, 0, stream);
+        }
         if (e != hipSuccess) return e;
       }
       if ((e = panel_q(p)) != hipSuccess) return e;

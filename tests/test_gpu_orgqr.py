@@ -58,6 +58,24 @@ def test_householder_product_matches_oracle(cuda, batch, n):
     _say(f"  ||Q-Qref||={err:.2e} ||QtQ-I||={orth:.2e} ||QR-A||/||A||={rec:.2e}")
 
 
+# batches of 48 and more, and tall matrices in batches of 16 or fewer, share one
+# update per four panels: full groups, a
+# ragged last group (n not a multiple of 128), a last panel narrower than 32
+@pytest.mark.parametrize("batch,n", [(48, 300), (50, 97), (64, 33), (48, 129), (49, 520), (16, 1057), (3, 1100)])
+def test_grouped_panels_match_oracle(cuda, batch, n):
+    _say(f"[orgqr grouped] batch={batch} n={n}")
+    a = gaussian(batch, n, 900 + n)
+    h, tau = custom_kernel(a.to(cuda))
+    q = fastqr.householder_product(h, tau)
+    torch.cuda.synchronize()
+    err, orth, rec = check_q(a, h, tau, q)
+    _say(f"  ||Q-Qref||={err:.2e} ||QtQ-I||={orth:.2e} ||QR-A||/||A||={rec:.2e}")
+    # the same factors one matrix at a time take the ungrouped path: same Q up to rounding
+    q1 = fastqr.householder_product(h[:1].contiguous(), tau[:1].contiguous())
+    torch.cuda.synchronize()
+    assert torch.linalg.matrix_norm((q1 - q[:1]).double()).max().item() <= 1e-5 * n
+
+
 def test_in_place_and_strided_factors_give_identical_q(cuda):
     a = gaussian(3, 200, 7).to(cuda)
     h, tau = custom_kernel(a)
