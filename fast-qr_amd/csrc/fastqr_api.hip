@@ -320,7 +320,9 @@ size_t fastqr_workspace_bytes(int64_t batch, int64_t n) {
 
 size_t fastqr_orgqr_workspace_bytes(int64_t batch, int64_t n) {
   if (batch <= 0 || n <= 0 || n > kMaxN) return 0;
-  return (fastqr::orgqr_workspace_floats(batch, (int)n) * sizeof(float) + 255) & ~(size_t)255;
+  // the batch is processed in chunks of at most kMaxGridY matrices
+  const int64_t chunk = batch < fastqr::kMaxGridY ? batch : fastqr::kMaxGridY;
+  return (fastqr::orgqr_workspace_floats(chunk, (int)n) * sizeof(float) + 255) & ~(size_t)255;
 }
 
 int fastqr_orgqr_f32(const float* H, int64_t batch, int64_t n, int64_t h_s0, int64_t h_s1, int64_t h_s2,
@@ -337,7 +339,7 @@ int fastqr_orgqr_f32(const float* H, int64_t batch, int64_t n, int64_t h_s0, int
   if (batch == 0 || n == 0) return FASTQR_OK;
   if (n > kMaxN) return fail(FASTQR_EINVAL, "n=%lld exceeds the supported maximum %lld", (long long)n,
                              (long long)kMaxN);
-  if (batch > 65535) return fail(FASTQR_EINVAL, "batch %lld exceeds 65535", (long long)batch);
+  if (batch > 2147483647LL) return fail(FASTQR_EINVAL, "batch too large");
   if (!H || !tau || !Q) return fail(FASTQR_EINVAL, "H, tau and Q must be non-null device pointers");
   if (h_s0 < 0 || h_s1 < 0 || h_s2 < 0 || q_s0 < 0 || q_s2 < 0 || tau_s0 < 0 || tau_s1 < 0)
     return fail(FASTQR_EINVAL, "negative strides are not supported");
@@ -364,9 +366,16 @@ int fastqr_orgqr_f32(const float* H, int64_t batch, int64_t n, int64_t h_s0, int
   if (ranges_overlap(tau, span_elems(batch, n, tau_s0, tau_s1, 0), Q, q_span))
     return fail(FASTQR_EOVERLAP, "tau and Q overlap");
   const bool vec = ((uintptr_t)Q % 16 == 0) && (q_s0 % 4 == 0) && (q_s2 % 4 == 0) && (n % 4 == 0);
-  const hipError_t e = fastqr::launch_orgqr(H, batch, (int)n, h_s0, h_s1, h_s2, tau, tau_s0, tau_s1, Q, q_s0, q_s2,
-                                            (float*)workspace, vec, (hipStream_t)stream_ptr);
-  return e == hipSuccess ? FASTQR_OK : hip_fail(e, "orgqr launch");
+  // chunks of at most kMaxGridY matrices (its kernels put the batch in grid.y),
+  // one after another on the stream, sharing the workspace
+  for (int64_t b0 = 0; b0 < batch; b0 += fastqr::kMaxGridY) {
+    const int64_t nb = (batch - b0 < fastqr::kMaxGridY) ? batch - b0 : fastqr::kMaxGridY;
+    const hipError_t e = fastqr::launch_orgqr(H + b0 * h_s0, nb, (int)n, h_s0, h_s1, h_s2, tau + b0 * tau_s0, tau_s0,
+                                              tau_s1, Q + b0 * q_s0, q_s0, q_s2, (float*)workspace, vec,
+                                              (hipStream_t)stream_ptr);
+    if (e != hipSuccess) return hip_fail(e, "orgqr launch");
+  }
+  return FASTQR_OK;
 }
 
 int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a_s1, int64_t a_s2,

@@ -17,6 +17,10 @@ hipError_t launch_qr_lds(const float* A, int64_t batch, int n, int64_t as0, int6
                          int64_t hs0, int64_t hs1, int64_t hs2, float* tau, int64_t ts0, int64_t ts1,
                          hipStream_t stream);
 
+// Largest grid.y (and grid.z) extent a launch uses: kernels that put the
+// batch there are launched in chunks of this many matrices.
+constexpr int64_t kMaxGridY = 65535;
+
 // Blocked path (qr_blocked.hip).
 // Copy columns [c0, c1) of A (any strides) into H (columns contiguous); c0 a
 // multiple of 64.

@@ -314,9 +314,15 @@ hipError_t launch_copy_colmajor(const float* A, int64_t batch, int n, int64_t as
   const int tj0 = c0 / 64, ntj = (c1 - c0 + 63) / 64;
   const bool vec = as2 == 1 && (as1 & 3) == 0 && (as0 & 3) == 0 && ((uintptr_t)A & 15) == 0 && (ldh & 3) == 0 &&
                    (hs0 & 3) == 0 && ((uintptr_t)H & 15) == 0 && (n & 3) == 0;
-  hipLaunchKernelGGL(copy_to_colmajor_kernel, dim3(ntile * ntj, (unsigned)batch), dim3(256), 0, stream, A,
-                     as0, as1, as2, H, hs0, ldh, n, ntile, tj0, vec);
-  return hipGetLastError();
+  // the batch goes to grid.y: at most kMaxGridY matrices per launch
+  for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
+    const int64_t nb = (batch - b0 < kMaxGridY) ? batch - b0 : kMaxGridY;
+    hipLaunchKernelGGL(copy_to_colmajor_kernel, dim3(ntile * ntj, (unsigned)nb), dim3(256), 0, stream, A + b0 * as0,
+                       as0, as1, as2, H + b0 * hs0, hs0, ldh, n, ntile, tj0, vec);
+    const hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return e;
+  }
+  return hipSuccess;
 }
 
 namespace {

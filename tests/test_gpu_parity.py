@@ -220,3 +220,25 @@ def test_geqrf_into_padded_leading_dimension(cuda, n):
     fastqr.geqrf_into(a.to(cuda), h, tau)
     torch.cuda.synchronize()
     assert torch.equal(h.cpu(), h_ref) and torch.equal(tau.cpu(), tau_ref)
+
+
+# Batches above 65535 matrices: the kernels that put the batch in grid.y are
+# launched in chunks; matrices on both sides of each chunk boundary are checked.
+@pytest.mark.parametrize("n", [8, 177])
+def test_batch_above_grid_y_limit(cuda, n):
+    batch = 65535 + 70
+    _say(f"[large batch] batch={batch} n={n}")
+    g = torch.Generator(device=cuda).manual_seed(4242)
+    a = torch.randn((batch, n, n), device=cuda, generator=g, dtype=torch.float32)
+    h, tau = custom_kernel(a)
+    torch.cuda.synchronize()
+    idx = torch.tensor([0, 1, 65533, 65534, 65535, 65536, batch - 1])
+    a_c, h_c, t_c = a[idx].cpu(), h[idx].cpu(), tau[idx].cpu()
+    assert_parity(a_c, h_c, t_c)
+    if n == 8:
+        import fastqr
+
+        q = fastqr.householder_product(h, tau)
+        torch.cuda.synchronize()
+        q_ref = torch.linalg.householder_product(h_c.double(), t_c.double())
+        assert torch.linalg.matrix_norm(q[idx].cpu().double() - q_ref).max().item() <= 1e-5 * n
