@@ -16,6 +16,7 @@
 //                       trailing-update kernels (which apply A - V T_s^T V^T A
 //                       with the stored T_s) apply B itself
 //   orgqr_panel_kernel  the panel's own columns, Q[r, k0+c] = d(r-k0, c) - V[r,:] Y[:, c]
+//   orgqr_small_kernel  n <= 32: all of the above for one matrix in one workgroup
 #include "device.hpp"
 #include "kernels.hpp"
 
@@ -182,6 +183,70 @@ __global__ void __launch_bounds__(256) orgqr_panel_kernel(float* __restrict__ Q,
 // on the row-split kernels, spread over row blocks (as geqrf's narrow updates).
 static bool orgqr_narrow_rowsplit(int64_t batch, int n) { return batch <= 16 && n > 1024; }
 
+// n <= 32 (a single panel): one workgroup of four waves per matrix does the
+// whole product in LDS, V read straight from H (any strides): G = V^T V, T (row i in lane i's
+// registers), Y = T V^T, Q = I - V Y.  Every read of H precedes the first
+// barrier and every write of Q follows it, so Q may be H itself.
+__global__ void __launch_bounds__(256) orgqr_small_kernel(const float* __restrict__ H, int64_t hs0, int64_t hs1,
+                                                         int64_t hs2, const float* __restrict__ tau, int64_t ts0,
+                                                         int64_t ts1, float* __restrict__ Q, int64_t qs0, int64_t ldq,
+                                                         int n) {
+  const int64_t b = blockIdx.x;
+  const int t = threadIdx.x;
+  __shared__ float Vs[32][33];
+  __shared__ float Gs[32][33];
+  __shared__ float Ts[32][33];
+  __shared__ float taus[32];
+  const float* Hb = H + b * hs0;
+  for (int e = t; e < 1024; e += 256) {
+    const int r = e & 31, c = e >> 5;
+    float x = 0.0f;
+    if (r < n && c < n) x = (r == c) ? 1.0f : (r < c ? 0.0f : Hb[r * hs1 + c * hs2]);
+    Vs[r][c] = x;
+  }
+  if (t < 32) taus[t] = (t < n) ? tau[b * ts0 + t * ts1] : 0.0f;
+  __syncthreads();
+  for (int e = t; e < 1024; e += 256) {
+    const int i = e >> 5, j = e & 31;
+    float g = 0.0f;
+#pragma unroll
+    for (int r = 0; r < 32; ++r) g = fmaf(Vs[r][i], Vs[r][j], g);
+    Gs[i][j] = g;
+  }
+  __syncthreads();
+  if (t < 32) {
+    const int i = t;
+    float trow[32];
+#pragma unroll
+    for (int j = 0; j < 32; ++j) {
+      float acc_s = 0.0f;
+#pragma unroll
+      for (int l = 0; l < j; ++l) acc_s = fmaf(trow[l], Gs[j][l], acc_s);  // G symmetric
+      const float tj = taus[j];
+      trow[j] = (i == j) ? tj : (i < j ? -tj * acc_s : 0.0f);
+    }
+#pragma unroll
+    for (int j = 0; j < 32; ++j) Ts[i][j] = trow[j];
+  }
+  __syncthreads();
+  for (int e = t; e < 1024; e += 256) {  // Y into Gs: Y(i, c) = sum_l T(i, l) V(c, l)
+    const int i = e >> 5, c = e & 31;
+    float y = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 32; ++l) y = fmaf(Ts[i][l], Vs[c][l], y);
+    Gs[i][c] = y;
+  }
+  __syncthreads();
+  float* Qb = Q + b * qs0;
+  for (int e = t; e < 1024; e += 256) {
+    const int r = e & 31, c = e >> 5;
+    float s = 0.0f;
+#pragma unroll
+    for (int l = 0; l < 32; ++l) s = fmaf(Vs[r][l], Gs[l][c], s);
+    if (r < n && c < n) Qb[c * ldq + r] = (r == c ? 1.0f : 0.0f) - s;
+  }
+}
+
 size_t orgqr_workspace_floats(int64_t batch, int n) {
   const int64_t npan = (n + 31) / 32;
   const int64_t nchunk = (npan + kMaxSlots - 1) / kMaxSlots;
@@ -193,6 +258,11 @@ size_t orgqr_workspace_floats(int64_t batch, int n) {
 hipError_t launch_orgqr(const float* H, int64_t batch, int n, int64_t hs0, int64_t hs1, int64_t hs2, const float* tau,
                         int64_t ts0, int64_t ts1, float* Q, int64_t qs0, int64_t ldq, float* ws, bool vec,
                         hipStream_t stream) {
+  if (n <= 32) {
+    hipLaunchKernelGGL(orgqr_small_kernel, dim3((unsigned)batch), dim3(256), 0, stream, H, hs0, hs1, hs2, tau, ts0, ts1,
+                       Q, qs0, ldq, n);
+    return hipGetLastError();
+  }
   const int npan = (n + 31) / 32;
   const int64_t nchunk = (npan + kMaxSlots - 1) / kMaxSlots;
   float* Tws = ws;

@@ -76,8 +76,9 @@ def test_grouped_panels_match_oracle(cuda, batch, n):
     assert torch.linalg.matrix_norm((q1 - q[:1]).double()).max().item() <= 1e-5 * n
 
 
-def test_in_place_and_strided_factors_give_identical_q(cuda):
-    a = gaussian(3, 200, 7).to(cuda)
+@pytest.mark.parametrize("n", [24, 200])
+def test_in_place_and_strided_factors_give_identical_q(cuda, n):
+    a = gaussian(3, n, 7).to(cuda)
     h, tau = custom_kernel(a)
     q = fastqr.householder_product(h, tau)
     hr = h.contiguous()  # row-major copy of the factors: any H strides are read
@@ -89,11 +90,12 @@ def test_in_place_and_strided_factors_give_identical_q(cuda):
     assert torch.equal(q, q_rm) and torch.equal(q, q_in)
 
 
-def test_zero_tau_gives_identity(cuda):
-    h = gaussian(2, 300, 9).to(cuda).transpose(-1, -2).contiguous().transpose(-1, -2)
-    q = fastqr.householder_product(h, torch.zeros((2, 300), device=cuda))
+@pytest.mark.parametrize("n", [20, 300])
+def test_zero_tau_gives_identity(cuda, n):
+    h = gaussian(2, n, 9).to(cuda).transpose(-1, -2).contiguous().transpose(-1, -2)
+    q = fastqr.householder_product(h, torch.zeros((2, n), device=cuda))
     torch.cuda.synchronize()
-    assert torch.equal(q.cpu(), torch.eye(300).expand(2, 300, 300))
+    assert torch.equal(q.cpu(), torch.eye(n).expand(2, n, n))
 
 
 @pytest.mark.parametrize("name,idx", [("C3", 0), ("C4", 0), ("C5", 0), ("C5", 1)])
