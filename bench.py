@@ -127,15 +127,15 @@ def summarize_traffic(fetch_dir: str, write_dir: str) -> str:
             ent[counter][0] += 1
             ent[counter][1] += kib * 1024.0 * factor
     lines = [
-        "# HBM traffic per launch — bench.py, all five workloads (one timed step)",
+        "# HBM traffic per launch — bench.py, all five workloads (one timed step, geqrf calls only)",
         "",
         "Commands (repository root on one MI355X; `$REPO` is the repository root):",
         "",
         "```",
         "cd /tmp && rocprofv3 --pmc FETCH_SIZE -d $REPO/gpurun_out/pmc_bfetch -o run -f csv -- python3 $REPO/bench.py "
-        "--steps 1 --warmup 0 --no-profile --no-check --cpu-sample-seconds 0 --calibrate-copy",
+        "--steps 1 --warmup 0 --no-profile --no-check --cpu-sample-seconds 0 --calibrate-copy --no-orgqr",
         "cd /tmp && rocprofv3 --pmc WRITE_SIZE -d $REPO/gpurun_out/pmc_bwrite -o run -f csv -- python3 $REPO/bench.py "
-        "--steps 1 --warmup 0 --no-profile --no-check --cpu-sample-seconds 0 --calibrate-copy",
+        "--steps 1 --warmup 0 --no-profile --no-check --cpu-sample-seconds 0 --calibrate-copy --no-orgqr",
         "python3 bench.py --summarize-traffic gpurun_out/pmc_bfetch gpurun_out/pmc_bwrite "
         "> profiles/hbm_traffic_bench_all_workloads.txt",
         "```",
@@ -192,6 +192,18 @@ def summarize_trace(path: str) -> str:
                   "|---|---:|---:|---:|---:|---:|"]
         for k, e in sorted(st.items(), key=lambda kv: -kv[1][1]):
             lines.append(f"| `{k}` | {e[0]} | {e[1] / e[0]:.2f} | {e[2]:.2f} | {e[3]:.2f} | {100 * e[1] / tot:.2f} |")
+        # per kernel family (all template instantiations): the wy_update_kernel
+        # row is the figure to set beside bench.py's HIP-event roofline average
+        fam = {}
+        for k, e in st.items():
+            base = k.split("<")[0]
+            f = "fastqr::wyr_* (row-split update)" if base.startswith("fastqr::wyr_") else base
+            a = fam.setdefault(f, [0, 0.0])
+            a[0] += e[0]
+            a[1] += e[1]
+        lines += ["", "| kernel family | calls | avg us | total ms |", "|---|---:|---:|---:|"]
+        for f, a in sorted(fam.items(), key=lambda kv: -kv[1][1]):
+            lines.append(f"| `{f}` | {a[0]} | {a[1] / a[0]:.2f} | {a[1] / 1e3:.1f} |")
         lines.append("")
     return "\n".join(lines)
 
