@@ -129,14 +129,14 @@ def summarize_traffic(fetch_dir: str, write_dir: str) -> str:
     lines = [
         "# HBM traffic per launch — bench.py, all five workloads (one timed step, geqrf calls only)",
         "",
-        "Commands (repository root on one MI355X; `$REPO` is the repository root):",
+        "Commands (repository root on one MI355X; `$REPO` is the repository root, `$OUT` an output directory):",
         "",
         "```",
-        "cd /tmp && rocprofv3 --pmc FETCH_SIZE -d $REPO/gpurun_out/pmc_bfetch -o run -f csv -- python3 $REPO/bench.py "
+        "cd /tmp && rocprofv3 --pmc FETCH_SIZE -d $OUT/pmc_bfetch -o run -f csv -- python3 $REPO/bench.py "
         "--steps 1 --warmup 0 --no-profile --no-check --cpu-sample-seconds 0 --calibrate-copy --no-orgqr",
-        "cd /tmp && rocprofv3 --pmc WRITE_SIZE -d $REPO/gpurun_out/pmc_bwrite -o run -f csv -- python3 $REPO/bench.py "
+        "cd /tmp && rocprofv3 --pmc WRITE_SIZE -d $OUT/pmc_bwrite -o run -f csv -- python3 $REPO/bench.py "
         "--steps 1 --warmup 0 --no-profile --no-check --cpu-sample-seconds 0 --calibrate-copy --no-orgqr",
-        "python3 bench.py --summarize-traffic gpurun_out/pmc_bfetch gpurun_out/pmc_bwrite "
+        "python3 bench.py --summarize-traffic $OUT/pmc_bfetch $OUT/pmc_bwrite "
         "> profiles/hbm_traffic_bench_all_workloads.txt",
         "```",
         "",
