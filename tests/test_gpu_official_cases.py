@@ -35,3 +35,43 @@ def test_official_case(cuda, case):
         assert torch.count_nonzero(tau) == 0
         assert torch.equal(h, a)
     print(f"  {msg}; {ag.message()}", flush=True)
+
+
+# The task's 12 benchmark cases (official/task.yml:109-121), each on a leading
+# sub-batch (the full batches are rechecked by bench.py after timing): the
+# structured 640 x 512 and 60 x 1024 batches and the mixed batches included.
+BENCH_LIMIT = {32: None, 176: None, 352: None, 512: 24, 1024: 6, 2048: 2, 4096: 1}
+
+
+@pytest.mark.parametrize("case", cases.BENCHMARKS, ids=[c.label for c in cases.BENCHMARKS])
+def test_official_benchmark_case(cuda, case):
+    limit = BENCH_LIMIT[case.n]
+    print(f"[official benchmark] {case.label} first {limit or case.batch}", flush=True)
+    a = cases.generate(case)
+    if limit is not None:
+        a = a[:limit].contiguous()
+    h, tau = custom_kernel(a.to(cuda))
+    torch.cuda.synchronize()
+    h, tau = h.cpu(), tau.cpu()
+    ok, msg = checker.official_check(a, h, tau)
+    assert ok, msg
+    h_ref, tau_ref = torch.geqrf(a)
+    ag = checker.rdiag_tau_agreement(a, h, tau, h_ref, tau_ref)
+    assert ag.ok, ag.message()
+
+
+# The explicit Q on every profile: fastqr.householder_product of the GPU
+# factors against the oracle (CPU torch.linalg.householder_product in fp64 of
+# the same factors), ||Q - Q_ref||_F <= 1e-5 n.
+@pytest.mark.parametrize("case", cases.TESTS, ids=[c.label for c in cases.TESTS])
+def test_official_case_explicit_q(cuda, case):
+    import fastqr
+
+    print(f"[official Q] {case.label}", flush=True)
+    a = cases.generate(case)
+    h, tau = custom_kernel(a.to(cuda))
+    q = fastqr.householder_product(h, tau)
+    torch.cuda.synchronize()
+    q_ref = torch.linalg.householder_product(h.cpu().double(), tau.cpu().double())
+    err = torch.linalg.matrix_norm(q.cpu().double() - q_ref).max().item()
+    assert err <= 1e-5 * case.n, f"||Q - Q_ref||_F = {err:.3e}"
