@@ -242,3 +242,26 @@ def test_batch_above_grid_y_limit(cuda, n):
         torch.cuda.synchronize()
         q_ref = torch.linalg.householder_product(h_c.double(), t_c.double())
         assert torch.linalg.matrix_norm(q[idx].cpu().double() - q_ref).max().item() <= 1e-5 * n
+
+
+# Batch isolation: NaN and Inf in some matrices leave every other matrix's
+# factors bit-identical to a clean run (strips of several matrices share the
+# update kernels' workgroups).
+@pytest.mark.parametrize("n", [32, 150, 600, 2100])
+def test_nonfinite_matrices_do_not_touch_others(cuda, n):
+    import fastqr
+
+    _say(f"[isolation] n={n}")
+    batch = 4 if n > 1024 else 12
+    a = gaussian(batch, n, 77 + n)
+    bad = a.clone()
+    bad[1, n // 2, n // 3] = float("nan")
+    bad[batch - 2, 0, 0] = float("inf")
+    h0, t0 = run_gpu(a, cuda)
+    h1, t1 = run_gpu(bad, cuda)
+    good = [i for i in range(batch) if i not in (1, batch - 2)]
+    assert torch.equal(h0[good], h1[good]) and torch.equal(t0[good], t1[good])
+    assert not torch.isfinite(h1[1]).all()
+    q0 = fastqr.householder_product(h0.to(cuda), t0.to(cuda)).cpu()
+    q1 = fastqr.householder_product(h1.to(cuda), t1.to(cuda)).cpu()
+    assert torch.equal(q0[good], q1[good])
