@@ -76,7 +76,7 @@ def test_grouped_panels_match_oracle(cuda, batch, n):
     assert torch.linalg.matrix_norm((q1 - q[:1]).double()).max().item() <= 1e-5 * n
 
 
-@pytest.mark.parametrize("n", [24, 200])
+@pytest.mark.parametrize("n", [24, 100, 200])
 def test_in_place_and_strided_factors_give_identical_q(cuda, n):
     a = gaussian(3, n, 7).to(cuda)
     h, tau = custom_kernel(a)
@@ -90,7 +90,7 @@ def test_in_place_and_strided_factors_give_identical_q(cuda, n):
     assert torch.equal(q, q_rm) and torch.equal(q, q_in)
 
 
-@pytest.mark.parametrize("n", [20, 300])
+@pytest.mark.parametrize("n", [20, 90, 300])
 def test_zero_tau_gives_identity(cuda, n):
     h = gaussian(2, n, 9).to(cuda).transpose(-1, -2).contiguous().transpose(-1, -2)
     q = fastqr.householder_product(h, torch.zeros((2, n), device=cuda))
