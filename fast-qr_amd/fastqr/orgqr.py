@@ -60,3 +60,21 @@ def householder_product(h: torch.Tensor, tau: torch.Tensor, *, out: torch.Tensor
     if rc != 0:
         raise FastQRError(rc, mod.last_error())
     return out
+
+
+def apply_q(h: torch.Tensor, tau: torch.Tensor, c: torch.Tensor, *, transpose: bool = False) -> torch.Tensor:
+    """Q C (or Q^T C with ``transpose``) for the geqrf factors ``(h, tau)``.
+
+    The meaning of ``torch.ormqr(h, tau, c, left=True, transpose=transpose)``
+    for square h with n reflectors and C of shape (batch, n, k): Q is formed
+    by ``householder_product`` (the HIP kernels) and applied with one batched
+    fp32 GEMM (``torch.bmm``, hipBLAS), a plain library product.
+    """
+    b, n = _check(h, tau)
+    if not isinstance(c, torch.Tensor) or c.dtype != torch.float32 or c.device != h.device:
+        raise TypeError("c must be a float32 tensor on h's device")
+    if c.dim() != 3 or c.shape[0] != b or c.shape[1] != n:
+        raise ValueError(f"c must have shape ({b}, {n}, k), got {tuple(c.shape)}")
+    q = householder_product(h, tau)
+    qm = q.transpose(-1, -2) if transpose else q
+    return torch.bmm(qm.contiguous(), c.contiguous())

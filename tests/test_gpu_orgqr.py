@@ -114,3 +114,25 @@ def test_full_workload_q_reconstructs_input(cuda, name, idx):
     _say(f"  max ||QR-A||/||A||={rec.max().item():.2e} max ||QtQ-I||={orth.max().item():.2e}")
     assert rec.max().item() <= 1e-5 * n
     assert orth.max().item() <= 1e-5 * n
+
+
+# Q C and Q^T C (torch.ormqr's meaning) against the oracle: CPU torch.ormqr in
+# fp64 on the same factors; tolerance ||X - X_ref||_F <= 1e-5 n ||C||_F.
+@pytest.mark.parametrize("batch,n,k,transpose", [(3, 20, 5, False), (3, 100, 100, True), (2, 600, 7, True),
+                                                 (2, 600, 7, False)])
+def test_apply_q_matches_ormqr(cuda, batch, n, k, transpose):
+    _say(f"[apply_q] batch={batch} n={n} k={k} transpose={transpose}")
+    a = gaussian(batch, n, 300 + n)
+    cm = gaussian(batch, max(n, k), 301 + n)[:, :n, :k].contiguous()
+    h, tau = custom_kernel(a.to(cuda))
+    x = fastqr.apply_q(h, tau, cm.to(cuda), transpose=transpose)
+    torch.cuda.synchronize()
+    x_ref = torch.ormqr(h.cpu().double(), tau.cpu().double(), cm.double(), left=True, transpose=transpose)
+    err = (torch.linalg.matrix_norm(x.cpu().double() - x_ref) / torch.linalg.matrix_norm(cm.double())).max().item()
+    assert err <= 1e-5 * n, f"||X - X_ref||_F / ||C||_F = {err:.3e}"
+    # Q^T (Q C) = C
+    if transpose:
+        back = fastqr.apply_q(h, tau, x, transpose=False)
+        torch.cuda.synchronize()
+        assert (torch.linalg.matrix_norm((back.cpu() - cm).double()) /
+                torch.linalg.matrix_norm(cm.double())).max().item() <= 1e-5 * n

@@ -254,3 +254,9 @@ def test_householder_product_rejects_bad_inputs_loudly():
         fastqr.householder_product(torch.zeros((2, 8, 7)), torch.zeros((2, 8)))
     with pytest.raises(ValueError):
         fastqr.householder_product(h, torch.zeros((2, 7)))
+
+
+def test_apply_q_rejects_bad_inputs_loudly():
+    h = torch.zeros((2, 8, 8))
+    with pytest.raises(ValueError):
+        fastqr.apply_q(h, torch.zeros((2, 8)), torch.zeros((2, 8, 3)))  # CPU tensors
