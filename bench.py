@@ -30,6 +30,7 @@ import json
 import math
 import os
 import statistics
+import subprocess
 import sys
 import time
 from pathlib import Path
@@ -72,6 +73,11 @@ def parse_args():
     p.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
                    help="print the HBM traffic summary of two rocprofv3 --pmc runs (FETCH_SIZE, WRITE_SIZE) of "
                         "this script with --calibrate-copy, and exit")
+    p.add_argument("--eval-contract", action="store_true",
+                   help="with --official: the evaluator's benchmark loop (official/eval.py:157-239): warm-up case, "
+                        "pre-timing check, up to 200 repeats with a cache flush each, stop once stderr/mean < 0.001 "
+                        "or the repeats reach 10 s, every repeat's outputs rechecked; Stats per case")
+    p.add_argument("--jsonl", metavar="PATH", help="with --eval-contract: append one provenance record per case")
     p.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                    help="print per-kernel statistics of a rocprofv3 --kernel-trace run of this script, split into "
                         "the geqrf calls and the householder_product calls, and exit")
@@ -230,6 +236,109 @@ def geomean(xs):
     return math.exp(sum(math.log(x) for x in xs) / len(xs)) if xs else float("nan")
 
 
+def eval_stats(durations):
+    """Stats of a list of per-call durations (official/eval.py:96-110)."""
+    runs = len(durations)
+    avg = sum(durations) / runs
+    std = math.sqrt(sum((x - avg) ** 2 for x in durations) / (runs - 1)) if runs > 1 else 0.0
+    err = std / math.sqrt(runs) if runs > 0 else 0.0
+    return {"runs": runs, "mean": avg, "std": std, "err": err, "best": min(durations), "worst": max(durations)}
+
+
+def run_eval_contract(args) -> int:
+    """The task's 12 benchmark cases under the evaluator's benchmark loop
+    (official/eval.py:157-239, restated).  Deviations, each stated in the
+    report: the cache flush writes 1 GiB (MI355X has a 256 MB Infinity Cache;
+    the evaluator writes 256 MiB), the pre-timing check runs the evaluator's
+    checker on the first 8 matrices of every input (on the CPU, in fp64), and
+    the per-repeat recheck compares every timed output bit for bit with the
+    checked one (the kernels are deterministic)."""
+    from dataclasses import replace
+
+    import torch
+
+    import fastqr
+    from fastqr import cases
+    from oracle import checker
+
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    torch.set_num_threads(len(os.sched_getaffinity(0)))
+    fastqr.ext()
+    flush_buf = torch.empty(FLUSH_BYTES // 8, dtype=torch.int64, device=dev)
+
+    def one_case(c, recheck, max_repeats, max_time_ns):
+        cnt = count_for(c.batch, c.n)
+        data = [cases.generate(replace(c, seed=c.seed + 42 * (i + 1))).to(dev) for i in range(cnt)]
+        ref = [tuple(t.clone() for t in fastqr.custom_kernel(d.clone())) for d in data]
+        torch.cuda.synchronize()
+        if recheck:
+            for d, (h, tau) in zip(data, ref):
+                k = min(c.batch, 8)
+                ok, msg = checker.official_check(d[:k].cpu(), h[:k].cpu(), tau[:k].cpu())
+                if not ok:
+                    return None, msg
+        durations = []
+        t_start = time.perf_counter_ns()
+        for i in range(max_repeats):
+            torch.cuda.synchronize()
+            flush_buf.fill_(42)
+            e0 = torch.cuda.Event(enable_timing=True)
+            e1 = torch.cuda.Event(enable_timing=True)
+            e0.record()
+            outs = [fastqr.custom_kernel(d) for d in data]
+            e1.record()
+            torch.cuda.synchronize()
+            durations.append(e0.elapsed_time(e1) * 1e6 / len(data))
+            if recheck:
+                for (h, tau), (hr, tr) in zip(outs, ref):
+                    if not (torch.equal(h, hr) and torch.equal(tau, tr)):
+                        return None, "a timed output differs from the checked one"
+            total = time.perf_counter_ns() - t_start
+            if i > 1 and total > 1e8:
+                st = eval_stats(durations)
+                if st["err"] / st["mean"] < 0.001 or st["mean"] * st["runs"] > max_time_ns or total > 120e9:
+                    break
+        return eval_stats(durations), None
+
+    one_case(cases.BENCHMARKS[0], False, 200, 1e8)  # warm-up (official/eval.py:228)
+    results, means, ok_all = {}, [], True
+    env = {"device": torch.cuda.get_device_name(0), "torch": torch.__version__, "hip": torch.version.hip}
+    try:
+        env["commit"] = subprocess.run(["git", "-C", str(ROOT), "rev-parse", "HEAD"], capture_output=True,
+                                       text=True, timeout=10).stdout.strip() or None
+    except (OSError, subprocess.SubprocessError):
+        env["commit"] = None
+    for idx, c in enumerate(cases.BENCHMARKS):
+        st, err = one_case(c, True, 200, 10e9)
+        if st is None:
+            ok_all = False
+            log(f"[eval] benchmark.{idx} {c.label}: FAIL {err}")
+            results[c.label] = {"status": "fail", "error": err}
+            continue
+        means.append(st["mean"])
+        results[c.label] = {k: (round(v, 1) if isinstance(v, float) else v) for k, v in st.items()}
+        log(f"[eval] benchmark.{idx} {c.label}: mean {st['mean'] / 1e3:.1f} us  err {st['err'] / 1e3:.2f} us  "
+            f"runs {st['runs']}")
+        if args.jsonl:
+            rec = {"spec": vars(c), "stats": st, "time": time.time(), **env}
+            with open(args.jsonl, "a") as fh:
+                fh.write(json.dumps(rec) + "\n")
+    value = geomean([m / 1e3 for m in means]) if ok_all else None
+    print(json.dumps({
+        "metric": METRIC_OFFICIAL + " (evaluator's benchmark loop)",
+        "value": None if value is None else round(value, 3),
+        "unit": "us/call (geomean of the cases' means)",
+        "n_gpus": 1,
+        "higher_is_better": False,
+        "dtype": "f32",
+        "data": "synthetic: the task's input profiles, restated, generated on the CPU",
+        "config": {"workload": "the 12 benchmark cases of the task (official/task.yml)", "cases_ns": results,
+                   "environment": env},
+    }), flush=True)
+    return 0 if ok_all else 3
+
+
 def main() -> int:
     args = parse_args()
     if args.summarize_traffic:
@@ -243,6 +352,11 @@ def main() -> int:
         log("bench.py measures one GPU only: every matrix is independent, so the path shards by batch "
             "with no communication; run with --gpus 1.")
         return 2
+    if args.eval_contract:
+        if not args.official:
+            log("--eval-contract needs --official")
+            return 2
+        return run_eval_contract(args)
 
     import torch
 
@@ -275,7 +389,8 @@ def main() -> int:
         groups = {f"B{i + 1:02d}": (c,) for i, c in enumerate(cases.BENCHMARKS)}
 
         def make_input(s, i):
-            return cases.generate(replace(s, seed=s.seed + 42 * i))
+            # official/eval.py:157-164: the seed advances by 42 before every input
+            return cases.generate(replace(s, seed=s.seed + 42 * (i + 1)))
     else:
         groups = {name.strip(): inputs.WORKLOADS[name.strip()] for name in args.configs.split(",") if name.strip()}
 
