@@ -356,7 +356,7 @@ int fastqr_orgqr_f32(const float* H, int64_t batch, int64_t n, int64_t h_s0, int
     return fail(FASTQR_ELAYOUT, "Q batch stride %lld smaller than one matrix (%lld)", (long long)q_s0,
                 (long long)(q_s2 * n));
   const size_t need = fastqr_orgqr_workspace_bytes(batch, n);
-  if (workspace_bytes < need || workspace == nullptr)
+  if (workspace_bytes < need || (need > 0 && workspace == nullptr))
     return fail(FASTQR_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
   if (((uintptr_t)workspace & 15) != 0) return fail(FASTQR_EWORKSPACE, "workspace must be 16-byte aligned");
   const bool same = ((const float*)Q == H && q_s0 == h_s0 && q_s1 == h_s1 && q_s2 == h_s2);

@@ -248,6 +248,7 @@ __global__ void __launch_bounds__(256) orgqr_small_kernel(const float* __restric
 }
 
 size_t orgqr_workspace_floats(int64_t batch, int n) {
+  if (n <= 32) return 0;  // orgqr_small_kernel: no scratch
   const int64_t npan = (n + 31) / 32;
   const int64_t nchunk = (npan + kMaxSlots - 1) / kMaxSlots;
   size_t f = 2 * (size_t)(nchunk * batch * kMaxSlots * 1024);

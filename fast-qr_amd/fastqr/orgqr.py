@@ -51,12 +51,12 @@ def householder_product(h: torch.Tensor, tau: torch.Tensor, *, out: torch.Tensor
         return out
     mod = ext()
     sptr = _current_stream_ptr(idx)
-    ws = workspace.scratch(h.device, sptr, mod.orgqr_workspace_bytes(b, n))
+    ws = workspace.scratch(h.device, sptr, mod.orgqr_workspace_bytes(b, n))  # None when none is needed
     hs0, hs1, hs2 = h.stride()
     ts0, ts1 = tau.stride()
     qs0, qs1, qs2 = out.stride()
     rc = mod.orgqr(h.data_ptr(), b, n, hs0, hs1, hs2, tau.data_ptr(), ts0, ts1, out.data_ptr(), qs0, qs1, qs2,
-                   ws.data_ptr(), ws.numel(), sptr)
+                   0 if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), sptr)
     if rc != 0:
         raise FastQRError(rc, mod.last_error())
     return out

@@ -95,7 +95,8 @@ size_t fastqr_workspace_bytes(int64_t batch, int64_t n);
  *        the two must not overlap.
  * workspace / workspace_bytes  at least fastqr_orgqr_workspace_bytes(batch, n)
  *        bytes of device scratch, 16-byte aligned (T and T V1^T per 32-column
- *        panel; for n > 2048 also the row-split partial products).
+ *        panel; for n > 2048 also the row-split partial products); may be
+ *        NULL when that size is 0 (n <= 32).
  * stream a hipStream_t; asynchronous, no host synchronisation.
  *
  * Returns FASTQR_OK, a negative FASTQR_E* argument error, or a positive
@@ -128,9 +129,10 @@ const char* fastqr_last_error(void);
 int fastqr_version(void);
 
 /*
- * Test hook: when `code` is non-zero the next fastqr_geqrf_f32 call on this
- * thread returns `code` without launching anything (used to test the host's
- * error path without faulting a GPU).  No counterpart in the reference.
+ * Test hook: when `code` is non-zero the next fastqr_geqrf_f32 or
+ * fastqr_orgqr_f32 call on this thread returns `code` without launching
+ * anything (used to test the host's error path without faulting a GPU).  No
+ * counterpart in the reference.
  */
 void fastqr_debug_force_error(int code);
 

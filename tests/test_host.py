@@ -224,6 +224,8 @@ def _orgqr_call(lib, H=8, b=2, n=100, h_s=None, tau=32, t_s=None, Q=16, q_s=None
 def test_orgqr_argument_validation_returns_codes_without_launching():
     lib = fastqr.cdll()
     assert lib.fastqr_orgqr_workspace_bytes(0, 64) == 0
+    assert lib.fastqr_orgqr_workspace_bytes(100000, 32) == 0  # one kernel, no scratch
+    assert _orgqr_call(lib, n=32, ws=0, ws_bytes=0, H=0) == _lib.FASTQR_EINVAL  # reaches the pointer check
     one = lib.fastqr_orgqr_workspace_bytes(1, 512)
     assert one > 0 and one % 256 == 0
     assert lib.fastqr_orgqr_workspace_bytes(640, 512) >= 640 * one - 255
