@@ -60,7 +60,10 @@ panel_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, float* __restrict_
   panel_body<NW, TPW, NBLK, VEC>(io, n - k0, (int)threadIdx.x);
 }
 
-int panel_width_for(int m) { return m > 2048 ? 16 : 32; }
+// 32-column panels up to 3072 rows ((8, 24, 2): 14 registers spill in the
+// 16-byte-load variant, still 64 fewer panels and narrow updates per 4096
+// matrix than 16 columns above 2048 rows: 2 x 4096 15.5 -> 14.5 ms on MI355X).
+int panel_width_for(int m) { return m > 3072 ? 16 : 32; }
 
 // Panels of the strip-resident path.  A 64-column panel updates its blocks
 // inside the kernel, which saves narrow trailing-update launches on the
@@ -96,6 +99,7 @@ hipError_t launch_panel_cfg(int nw, int tpw, float* H, int64_t batch, int64_t hs
   FASTQR_PANEL(4, 8, 2)
   FASTQR_PANEL(4, 16, 2)
   FASTQR_PANEL(8, 16, 2)
+  FASTQR_PANEL(8, 24, 2)
   FASTQR_PANEL(8, 16, 1)
   FASTQR_PANEL(8, 32, 1)
   FASTQR_PANEL(8, 8, 2)
@@ -147,6 +151,8 @@ hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float
       nw = 8, tpw = 8;
     } else if (m <= 2048) {
       nw = 8, tpw = 16;
+    } else if (m <= 3072) {
+      nw = 8, tpw = 24;
     }
   } else if (nb == 16) {
     if (m <= 2048) {
