@@ -136,3 +136,12 @@ def test_apply_q_matches_ormqr(cuda, batch, n, k, transpose):
         torch.cuda.synchronize()
         assert (torch.linalg.matrix_norm((back.cpu() - cm).double()) /
                 torch.linalg.matrix_norm(cm.double())).max().item() <= 1e-5 * n
+
+
+def test_forced_error_in_householder_product_surfaces(cuda):
+    h = torch.randn((2, 40, 40), device=cuda)
+    tau = torch.zeros((2, 40), device=cuda)
+    fastqr.cdll().fastqr_debug_force_error(-99)
+    with pytest.raises(fastqr.FastQRError) as exc:
+        fastqr.householder_product(h, tau)
+    assert exc.value.code == -99

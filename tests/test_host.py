@@ -262,3 +262,15 @@ def test_apply_q_rejects_bad_inputs_loudly():
     h = torch.zeros((2, 8, 8))
     with pytest.raises(ValueError):
         fastqr.apply_q(h, torch.zeros((2, 8)), torch.zeros((2, 8, 3)))  # CPU tensors
+
+
+def test_missing_native_library_fails_loudly(monkeypatch, tmp_path):
+    # no fallback: without the library every entry point raises
+    monkeypatch.setattr(_lib, "LIB_PATH", tmp_path / "libfastqr.so")
+    monkeypatch.setattr(_lib, "EXT_PATH", tmp_path / "_fastqr_py.so")
+    monkeypatch.setattr(_lib, "_cdll", None)
+    monkeypatch.setattr(_lib, "_ext", None)
+    with pytest.raises(fastqr.FastQRUnavailable):
+        _lib.cdll()
+    with pytest.raises(fastqr.FastQRUnavailable):
+        _lib.ext()
