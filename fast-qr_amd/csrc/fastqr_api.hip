@@ -480,7 +480,16 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   // one scratch area: narrow updates run one at a time, on the side stream
   const bool wyr_narrow = use_wyr_narrow(batch, n);
   float* const wyr_scratch = Tws + (size_t)batch * fastqr::kMaxSlots * 1024;
+  // Narrow updates inside a group, left-looking: after each panel only the
+  // next panel's columns are updated, by all of the group's transforms so far
+  // in one launch (the later columns wait for their own turn), so the launch
+  // on the critical path covers one panel instead of the rest of the group and
+  // loads its columns once for several transforms.  Groups whose narrow
+  // updates run on the row-split kernels keep one transform per launch over
+  // the rest of the group (those kernels join several transforms only with a
+  // group T).
   auto run_panels = [&](const Group& G, hipStream_t st) -> hipError_t {
+    const bool left_looking = !(wyr_narrow && ni - G.g0 > kWyrNarrowMinRows);
     for (int pk = G.g0; pk < G.g_end; pk += G.pw) {
       const double m = ni - pk;
       const int wi = (G.g_end - pk < G.pw) ? G.g_end - pk : G.pw;
@@ -492,7 +501,18 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
       });
       if (err != hipSuccess) return err;
       const int c0 = pk + wi;
-      if (c0 < G.g_end) {
+      if (c0 < G.g_end && left_looking) {
+        const int c1 = (G.g_end - c0 < G.pw) ? G.g_end : c0 + G.pw;  // the next panel's columns
+        const int nwy = (c0 - G.g0) / kTw;                              // transforms of the group so far
+        double fl = 0.0;
+        for (int j = 0; j < nwy; ++j) fl += 4.0 * (ni - G.g0 - kTw * j) * kTw * (c1 - c0);
+        const double mg = ni - G.g0;
+        err = timed(kUpdate, bd * fl, bd * (8.0 * mg * (c1 - c0) + 4.0 * mg * (c0 - G.g0)), st, [&] {
+          return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, G.g0, kTw, G.slot_base, nwy, c0, c1, vec,
+                                          true, 0, st);
+        });
+        if (err != hipSuccess) return err;
+      } else if (c0 < G.g_end) {
         const double c = G.g_end - c0;
         if (wyr_narrow && wi <= kTw && ni - pk > kWyrNarrowMinRows) {
           fastqr::WyrCall wc{};
