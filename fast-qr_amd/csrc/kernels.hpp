@@ -92,6 +92,9 @@ constexpr int kMaxSlots = 3 * kMaxWY;
 // updates run on the row-split kernels.
 constexpr int kOrgqrRowSplitMinN = 2048;
 constexpr int64_t kOrgqrGroupMinBatch = 48;  // panels grouped per update from this batch on
+// from this batch on, a group's narrow updates are left-looking (one column
+// block per launch, every earlier transform of the group at once)
+constexpr int64_t kOrgqrLeftLookingMinBatch = 256;
 size_t orgqr_workspace_floats(int64_t batch, int n);
 hipError_t launch_orgqr(const float* H, int64_t batch, int n, int64_t hs0, int64_t hs1, int64_t hs2, const float* tau,
                         int64_t ts0, int64_t ts1, float* Q, int64_t qs0, int64_t ldq, float* ws, bool vec,

@@ -60,8 +60,11 @@ def test_householder_product_matches_oracle(cuda, batch, n):
 
 # batches of 48 and more, and tall matrices in batches of 16 or fewer, share one
 # update per four panels: full groups, a
-# ragged last group (n not a multiple of 128), a last panel narrower than 32
-@pytest.mark.parametrize("batch,n", [(48, 300), (50, 97), (64, 33), (48, 129), (49, 520), (16, 1057), (3, 1100)])
+# ragged last group (n not a multiple of 128), a last panel narrower than 32;
+# from batch 256 on the group's narrow updates are left-looking (a last
+# column block of one column, a ragged last group)
+@pytest.mark.parametrize("batch,n", [(48, 300), (50, 97), (64, 33), (48, 129), (49, 520), (16, 1057), (3, 1100),
+                                     (256, 97), (300, 200), (260, 300)])
 def test_grouped_panels_match_oracle(cuda, batch, n):
     _say(f"[orgqr grouped] batch={batch} n={n}")
     a = gaussian(batch, n, 900 + n)
