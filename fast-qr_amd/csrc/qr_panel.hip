@@ -110,6 +110,11 @@ hipError_t launch_panel_cfg(int nw, int tpw, float* H, int64_t batch, int64_t hs
   FASTQR_PANEL(4, 4, 4)
   FASTQR_PANEL(4, 8, 4)
   FASTQR_PANEL(8, 8, 4)
+  FASTQR_PANEL(4, 6, 2)
+  FASTQR_PANEL(8, 6, 2)
+  FASTQR_PANEL(8, 12, 2)
+  FASTQR_PANEL(4, 6, 4)
+  FASTQR_PANEL(8, 6, 4)
 #undef FASTQR_PANEL
   return hipErrorInvalidValue;
 }
@@ -133,8 +138,12 @@ hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float
   } else if (nb == 64) {
     if (m <= 256) {
       nw = 4, tpw = 4;
+    } else if (m <= 384) {
+      nw = 4, tpw = 6;
     } else if (m <= 512) {
       nw = 4, tpw = 8;
+    } else if (m <= 768) {
+      nw = 8, tpw = 6;
     } else if (m <= 1024) {
       nw = 8, tpw = 8;
     }
@@ -145,10 +154,16 @@ hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float
       nw = 2, tpw = 4;
     } else if (m <= 256) {
       nw = 4, tpw = 4;
+    } else if (m <= 384) {
+      nw = 4, tpw = 6;
     } else if (m <= 512) {
       nw = 4, tpw = 8;
+    } else if (m <= 768) {
+      nw = 8, tpw = 6;
     } else if (m <= 1024) {
       nw = 8, tpw = 8;
+    } else if (m <= 1536) {
+      nw = 8, tpw = 12;
     } else if (m <= 2048) {
       nw = 8, tpw = 16;
     } else if (m <= 3072) {
