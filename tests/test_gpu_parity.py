@@ -224,6 +224,25 @@ def test_geqrf_into_padded_leading_dimension(cuda, n):
 
 # Batches above 65535 matrices: the kernels that put the batch in grid.y are
 # launched in chunks; matrices on both sides of each chunk boundary are checked.
+# From batch 512 on the blocked path takes 32-column panels in groups of four
+# with left-looking narrow updates; n = 400 and 700 reach the panel height
+# classes of 384, 512 and 768 rows. Matrices across the batch against the oracle.
+@pytest.mark.parametrize("n", [400, 700])
+def test_large_batch_thirty_two_column_panels(cuda, n):
+    batch = 512
+    _say(f"[large batch panels] batch={batch} n={n}")
+    g = torch.Generator(device=cuda).manual_seed(515 + n)
+    a = torch.randn((batch, n, n), device=cuda, generator=g, dtype=torch.float32)
+    h, tau = custom_kernel(a)
+    torch.cuda.synchronize()
+    idx = torch.tensor([0, 1, 255, 256, 383, batch - 1])
+    a_c, h_c, t_c = a[idx].cpu(), h[idx].cpu(), tau[idx].cpu()
+    ag = assert_parity(a_c, h_c, t_c)
+    _say(f"  {ag.message()}")
+    del a, h, tau
+    torch.cuda.empty_cache()
+
+
 @pytest.mark.parametrize("n", [8, 177])
 def test_batch_above_grid_y_limit(cuda, n):
     batch = 65535 + 70
