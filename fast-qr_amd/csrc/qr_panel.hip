@@ -115,6 +115,8 @@ hipError_t launch_panel_cfg(int nw, int tpw, float* H, int64_t batch, int64_t hs
   FASTQR_PANEL(8, 12, 2)
   FASTQR_PANEL(4, 6, 4)
   FASTQR_PANEL(8, 6, 4)
+  FASTQR_PANEL(4, 2, 4)
+  FASTQR_PANEL(4, 3, 4)
 #undef FASTQR_PANEL
   return hipErrorInvalidValue;
 }
@@ -136,7 +138,13 @@ hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float
       nw = 8, tpw = 4;
     }
   } else if (nb == 64) {
-    if (m <= 256) {
+    if (m <= 64) {
+      nw = 1, tpw = 4;
+    } else if (m <= 128) {
+      nw = 4, tpw = 2;
+    } else if (m <= 192) {
+      nw = 4, tpw = 3;
+    } else if (m <= 256) {
       nw = 4, tpw = 4;
     } else if (m <= 384) {
       nw = 4, tpw = 6;
