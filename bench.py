@@ -68,6 +68,8 @@ def parse_args():
     p.add_argument("--official", action="store_true",
                    help="time the task's own 12 benchmark cases (official/task.yml) instead of the five workloads; "
                         "value = geomean over the 12 cases")
+    p.add_argument("--no-colmajor", action="store_true",
+                   help="skip the column-major input leg of C2 (40 x 176, 40 x 352 as column-major views)")
     p.add_argument("--calibrate-copy", action="store_true",
                    help="start with a plain 256 MiB device copy (the reference kernel for HBM counter scaling)")
     p.add_argument("--summarize-traffic", nargs=2, metavar=("FETCH_DIR", "WRITE_DIR"),
@@ -78,6 +80,9 @@ def parse_args():
                         "pre-timing check, up to 200 repeats with a cache flush each, stop once stderr/mean < 0.001 "
                         "or the repeats reach 10 s, every repeat's outputs rechecked; Stats per case")
     p.add_argument("--jsonl", metavar="PATH", help="with --eval-contract: append one provenance record per case")
+    p.add_argument("--eval-cases", metavar="I,J,...", help="with --eval-contract: only these benchmark cases (0-based)")
+    p.add_argument("--eval-max-time-ns", type=float, default=10e9,
+                   help="with --eval-contract: per-case kernel-time budget of the stopping rule (evaluator: 10 s)")
     p.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                    help="print per-kernel statistics of a rocprofv3 --kernel-trace run of this script, split into "
                         "the geqrf calls and the householder_product calls, and exit")
@@ -91,6 +96,27 @@ TRAFFIC_SUMMARY = "hbm_traffic_bench_all_workloads.txt"
 CALIB_BYTES = 256 * 1024 * 1024
 KIND_OF = (("panel_kernel", "panel"), ("wy_update_kernel", "update"), ("wyr_", "update_rowsplit"),
            ("copy_to_colmajor", "copy"), ("qr_wave_kernel", "wave64"), ("qr_lds_kernel", "lds"))
+
+
+# Roofline each kernel kind is held to: (bound, peak, unit).  The panel is
+# VALU work (fp32 vector peak = fp32 MFMA peak on MI355X); the copy, wave64
+# and LDS-resident kernels are priced by their algorithmic HBM bytes.
+KIND_BOUND = {
+    "update": ("mfma", PEAK_FP32_TFLOPS, "TFLOP/s"),
+    "update_rowsplit": ("mfma", PEAK_FP32_TFLOPS, "TFLOP/s"),
+    "panel": ("valu", PEAK_FP32_TFLOPS, "TFLOP/s"),
+    "copy": ("hbm", PEAK_HBM_GBS, "GB/s"),
+    "wave64": ("hbm", PEAK_HBM_GBS, "GB/s"),
+    "lds": ("hbm", PEAK_HBM_GBS, "GB/s"),
+}
+KIND_KERNEL = {
+    "update": "wy_update_kernel (trailing update A2 -= V T^T V^T A2, v_mfma_f32_32x32x2f32)",
+    "update_rowsplit": "wyr_* (row-split trailing update of tall matrices: partial V^T X, T, W, apply)",
+    "panel": "panel_kernel (panel factorisation and T factor, one workgroup per matrix)",
+    "copy": "copy_to_colmajor_kernel (A -> column-major H)",
+    "wave64": "qr_wave_kernel (n <= 64, one wave64 per matrix)",
+    "lds": "qr_lds_kernel (64 < n <= 176, matrix resident in LDS)",
+}
 
 
 def _counter_rows(directory: str, counter: str):
@@ -247,83 +273,52 @@ def eval_stats(durations):
 
 def run_eval_contract(args) -> int:
     """The task's 12 benchmark cases under the evaluator's benchmark loop
-    (official/eval.py:157-239, restated).  Deviations, each stated in the
-    report: the cache flush writes 1 GiB (MI355X has a 256 MB Infinity Cache;
-    the evaluator writes 256 MiB), the pre-timing check runs the evaluator's
-    checker on the first 8 matrices of every input (on the CPU, in fp64), and
-    the per-repeat recheck compares every timed output bit for bit with the
-    checked one (the kernels are deterministic)."""
-    from dataclasses import replace
-
+    (official/eval.py:157-251, restated in fastqr.evaluator).  Deviations,
+    each stated in the report: the cache flush writes 1 GiB (MI355X has a
+    256 MB Infinity Cache; the evaluator writes 256 MiB), the pre-timing check
+    runs the evaluator's checker on the first 8 matrices of every input (on
+    the CPU, in fp64), and the per-repeat recheck compares every timed output
+    bit for bit with the checked one (the kernels are deterministic)."""
     import torch
 
     import fastqr
-    from fastqr import cases
+    from fastqr import cases, evaluator
     from oracle import checker
 
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     torch.set_num_threads(len(os.sched_getaffinity(0)))
     fastqr.ext()
-    flush_buf = torch.empty(FLUSH_BYTES // 8, dtype=torch.int64, device=dev)
-
-    def one_case(c, recheck, max_repeats, max_time_ns):
-        cnt = count_for(c.batch, c.n)
-        data = [cases.generate(replace(c, seed=c.seed + 42 * (i + 1))).to(dev) for i in range(cnt)]
-        ref = [tuple(t.clone() for t in fastqr.custom_kernel(d.clone())) for d in data]
-        torch.cuda.synchronize()
-        if recheck:
-            for d, (h, tau) in zip(data, ref):
-                k = min(c.batch, 8)
-                ok, msg = checker.official_check(d[:k].cpu(), h[:k].cpu(), tau[:k].cpu())
-                if not ok:
-                    return None, msg
-        durations = []
-        t_start = time.perf_counter_ns()
-        for i in range(max_repeats):
-            torch.cuda.synchronize()
-            flush_buf.fill_(42)
-            e0 = torch.cuda.Event(enable_timing=True)
-            e1 = torch.cuda.Event(enable_timing=True)
-            e0.record()
-            outs = [fastqr.custom_kernel(d) for d in data]
-            e1.record()
-            torch.cuda.synchronize()
-            durations.append(e0.elapsed_time(e1) * 1e6 / len(data))
-            if recheck:
-                for (h, tau), (hr, tr) in zip(outs, ref):
-                    if not (torch.equal(h, hr) and torch.equal(tau, tr)):
-                        return None, "a timed output differs from the checked one"
-            total = time.perf_counter_ns() - t_start
-            if i > 1 and total > 1e8:
-                st = eval_stats(durations)
-                if st["err"] / st["mean"] < 0.001 or st["mean"] * st["runs"] > max_time_ns or total > 120e9:
-                    break
-        return eval_stats(durations), None
-
-    one_case(cases.BENCHMARKS[0], False, 200, 1e8)  # warm-up (official/eval.py:228)
-    results, means, ok_all = {}, [], True
+    specs = list(cases.BENCHMARKS)
+    if args.eval_cases:
+        specs = [specs[int(i)] for i in args.eval_cases.split(",")]
+    device = evaluator.torch_device(torch, fastqr.custom_kernel, checker.official_check, FLUSH_BYTES)
     env = {"device": torch.cuda.get_device_name(0), "torch": torch.__version__, "hip": torch.version.hip}
     try:
         env["commit"] = subprocess.run(["git", "-C", str(ROOT), "rev-parse", "HEAD"], capture_output=True,
                                        text=True, timeout=10).stdout.strip() or None
     except (OSError, subprocess.SubprocessError):
         env["commit"] = None
-    for idx, c in enumerate(cases.BENCHMARKS):
-        st, err = one_case(c, True, 200, 10e9)
-        if st is None:
-            ok_all = False
-            log(f"[eval] benchmark.{idx} {c.label}: FAIL {err}")
-            results[c.label] = {"status": "fail", "error": err}
-            continue
-        means.append(st["mean"])
+    results = {}
+
+    def on_result(idx, c, res):
+        if not isinstance(res, evaluator.Stats):
+            log(f"[eval] benchmark.{idx} {c.label}: FAIL {res}")
+            results[c.label] = {"status": "fail", "error": res}
+            return
+        st = vars(res)
         results[c.label] = {k: (round(v, 1) if isinstance(v, float) else v) for k, v in st.items()}
-        log(f"[eval] benchmark.{idx} {c.label}: mean {st['mean'] / 1e3:.1f} us  err {st['err'] / 1e3:.2f} us  "
-            f"runs {st['runs']}")
+        log(f"[eval] benchmark.{idx} {c.label}: mean {res.mean / 1e3:.1f} us  err {res.err / 1e3:.2f} us  "
+            f"runs {res.runs}")
         if args.jsonl:
             rec = {"spec": vars(c), "stats": st, "time": time.time(), **env}
             with open(args.jsonl, "a") as fh:
                 fh.write(json.dumps(rec) + "\n")
+
+    out, ok_all = evaluator.run_benchmarking(specs, lambda c: cases.generate(c).to(dev), device, recheck="bitwise",
+                                             check_matrices=8, max_time_ns=args.eval_max_time_ns,
+                                             on_result=on_result)
+    means = [r.mean for r in out if isinstance(r, evaluator.Stats)]
     value = geomean([m / 1e3 for m in means]) if ok_all else None
     print(json.dumps({
         "metric": METRIC_OFFICIAL + " (evaluator's benchmark loop)",
@@ -439,6 +434,36 @@ def main() -> int:
     wall = time.perf_counter() - wall0
     for label, e0, e1, cnt in events:
         per_shape_us[label].append(e0.elapsed_time(e1) * 1e3 / cnt)
+
+    # ---- C2 with column-major inputs (the layout BASELINE C2 names): the same
+    # values as column-major views, timed like the headline shapes ----------------
+    colmajor = {}
+    if not args.official and not args.no_colmajor and "C2" in groups:
+        for s in groups["C2"]:
+            cm = [d.transpose(1, 2).contiguous().transpose(1, 2) for d in data[s.label]]
+            for d in cm[:1]:
+                fastqr.custom_kernel(d)
+            torch.cuda.synchronize()
+            times = []
+            for _ in range(max(1, args.steps)):
+                flush_buf.fill_(42)
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                outs = [fastqr.custom_kernel(d) for d in cm]
+                e1.record()
+                torch.cuda.synchronize()
+                times.append(e0.elapsed_time(e1) * 1e3 / len(cm))
+            h_cm, t_cm = outs[-1]
+            h_rm, t_rm = fastqr.custom_kernel(data[s.label][-1])
+            torch.cuda.synchronize()
+            same = bool(torch.equal(h_cm, h_rm) and torch.equal(t_cm, t_rm))
+            us = statistics.median(times)
+            colmajor[s.label] = {"us_per_call": round(us, 3), "best_us": round(min(times), 3),
+                                 "gflops": round(inputs.flops(s.batch, s.n) / (us * 1e-6) / 1e9, 2),
+                                 "stride": list(cm[0].stride()), "bitwise_equal_to_row_major": same}
+            log(f"[gpu] C2 {s.label} column-major: {us:9.1f} us/call  (bitwise equal to row-major: {same})")
+            del cm, outs
 
     # ---- recheck (last timed outputs of every shape) ---------------------------
     checks = {}
@@ -586,36 +611,50 @@ def main() -> int:
     value = geomean(list(cfg_us.values()))
     cpu_value = geomean(list(cfg_cpu.values())) if cfg_cpu else None
 
-    # roofline of the dominant kernel (the fp32-MFMA trailing update) over the workload
+    # roofline of each kernel kind over the workload (algorithmic work per
+    # launch / average launch duration from the library's HIP events); the
+    # headline `roofline` is the kind with the largest share of kernel time
     roof = None
+    roof_by_kind = {}
     if kernels:
-        agg = {"launches": 0, "ms": 0.0, "flops": 0.0, "bytes": 0.0}
-        per_kind_ms = {}
+        agg = {}
         for label, kd in kernels.items():
             for kname, st in kd.items():
-                per_kind_ms[kname] = per_kind_ms.get(kname, 0.0) + st["ms"]
-            st = kd.get("update", {})
-            for f in agg:
-                agg[f] += st.get(f, 0)
-        if agg["launches"] and agg["ms"] > 0:
-            avg_s = agg["ms"] * 1e-3 / agg["launches"]
-            achieved = agg["flops"] / agg["launches"] / avg_s / 1e12
-            roof = {
-                "bound": "mfma",
-                "kernel": "wy_update_kernel (trailing update A2 -= V T^T V^T A2, v_mfma_f32_32x32x2f32), "
-                          "all launches of all workloads",
-                "achieved": round(achieved, 2),
-                "peak": PEAK_FP32_TFLOPS,
-                "unit": "TFLOP/s",
-                "frac": round(achieved / PEAK_FP32_TFLOPS, 4),
-                "traffic": traffic_per_launch(args.traffic_file, "update"),
-                "traffic_source": os.path.relpath(args.traffic_file, ROOT),
-                "launches": agg["launches"],
+                a = agg.setdefault(kname, {"launches": 0, "ms": 0.0, "flops": 0.0, "bytes": 0.0})
+                for f in a:
+                    a[f] += st.get(f, 0)
+        tot_ms = sum(a["ms"] for a in agg.values()) or 1.0
+        for kname, a in agg.items():
+            if not a["launches"] or a["ms"] <= 0:
+                continue
+            bound, peak, unit = KIND_BOUND[kname]
+            avg_s = a["ms"] * 1e-3 / a["launches"]
+            work = a["flops"] if bound != "hbm" else a["bytes"]
+            achieved = work / a["launches"] / avg_s / (1e12 if unit == "TFLOP/s" else 1e9)
+            roof_by_kind[kname] = {
+                "bound": bound,
+                "kernel": KIND_KERNEL[kname],
+                "achieved": round(achieved, 3),
+                "peak": peak,
+                "unit": unit,
+                "frac": round(achieved / peak, 4),
+                "traffic": traffic_per_launch(args.traffic_file, kname),
+                "launches": a["launches"],
                 "avg_launch_us": round(avg_s * 1e6, 3),
-                "flops_per_launch": agg["flops"] / agg["launches"],
-                "time_share_by_kernel": {k: round(v / sum(per_kind_ms.values()), 3) for k, v in per_kind_ms.items()
-                                         if v > 0},
+                "work_per_launch": work / a["launches"],
+                "time_share": round(a["ms"] / tot_ms, 3),
             }
+        if roof_by_kind:
+            dom = max(roof_by_kind, key=lambda k: roof_by_kind[k]["time_share"])
+            roof = dict(roof_by_kind[dom])
+            roof["kind"] = dom
+            if roof["bound"] == "valu":
+                # compute-bound on the vector ALUs: MI355X's fp32 vector peak is
+                # its fp32 MFMA peak, so the compute roof is the same
+                roof["bound"] = "mfma"
+                roof["compute_units"] = "valu (fp32 vector peak = fp32 MFMA peak)"
+            roof["traffic_source"] = os.path.relpath(args.traffic_file, ROOT)
+            roof["time_share_by_kernel"] = {k: v["time_share"] for k, v in roof_by_kind.items()}
 
     line = {
         "metric": METRIC_OFFICIAL if args.official else METRIC,
@@ -641,8 +680,10 @@ def main() -> int:
             "householder_product_geomean_shapes_us": (round(geomean(list(orgqr_us.values())), 3)
                                                       if orgqr_us else None),
             "shapes": shape_rows,
+            "c2_column_major": colmajor or None,
         },
         "roofline": roof,
+        "roofline_by_kernel": roof_by_kind or None,
         "cpu_baseline": None if cpu_value is None else {
             "value": round(cpu_value, 1),
             "unit": "us/call (geomean over configs)",

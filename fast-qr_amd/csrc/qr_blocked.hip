@@ -22,10 +22,13 @@ namespace fastqr {
 // ---------------------------------------------------------------------------
 // A (any strides) -> H (columns contiguous, leading dimension ldh)
 // ---------------------------------------------------------------------------
+// Copy modes: element loads (any strides), 16-byte row segments transposed
+// through LDS (row-major source), 16-byte column segments (column-major).
+constexpr int kCopyScalar = 0, kCopyRowVec = 1, kCopyColVec = 2;
 __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __restrict__ A, int64_t as0,
                                                                 int64_t as1, int64_t as2,
                                                                 float* __restrict__ H, int64_t hs0,
-                                                                int64_t ldh, int n, int ntile, int tj0, bool vec) {
+                                                                int64_t ldh, int n, int ntile, int tj0, int mode) {
   __shared__ float tile[64][65];
   const int64_t b = blockIdx.y;
   const int ti = blockIdx.x % ntile;
@@ -33,7 +36,27 @@ __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __re
   const float* Ab = A + b * as0;
   float* Hb = H + b * hs0;
   const int tid = threadIdx.x;
-  if (vec) {
+  if (mode == kCopyColVec) {
+    // column-major source, columns 16-byte aligned and n a multiple of 4: no
+    // transpose, each thread moves four 16-byte column segments straight
+    // through (16 threads cover 256 contiguous bytes of a column)
+    const int i4 = 4 * (tid & 15);
+    f32x4 v[4];
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int j = (tid >> 4) + 16 * k;
+      const int gi = ti * 64 + i4, gj = tj * 64 + j;
+      if (gi < n && gj < n) v[k] = *reinterpret_cast<const f32x4*>(Ab + (int64_t)gj * as2 + gi);
+    }
+#pragma unroll
+    for (int k = 0; k < 4; ++k) {
+      const int j = (tid >> 4) + 16 * k;
+      const int gi = ti * 64 + i4, gj = tj * 64 + j;
+      if (gi < n && gj < n) *reinterpret_cast<f32x4*>(Hb + (int64_t)gj * ldh + gi) = v[k];
+    }
+    return;
+  }
+  if (mode == kCopyRowVec) {
     // row-major source, every row and column a multiple of 16 bytes: each
     // thread moves four 16-byte row segments in and four column segments out
     const int c4 = 4 * (tid & 15);
@@ -312,13 +335,16 @@ hipError_t launch_copy_colmajor(const float* A, int64_t batch, int n, int64_t as
   if (c1 <= c0) return hipSuccess;
   const int ntile = (n + 63) / 64;
   const int tj0 = c0 / 64, ntj = (c1 - c0 + 63) / 64;
-  const bool vec = as2 == 1 && (as1 & 3) == 0 && (as0 & 3) == 0 && ((uintptr_t)A & 15) == 0 && (ldh & 3) == 0 &&
-                   (hs0 & 3) == 0 && ((uintptr_t)H & 15) == 0 && (n & 3) == 0;
+  const bool h_vec = (ldh & 3) == 0 && (hs0 & 3) == 0 && ((uintptr_t)H & 15) == 0 && (n & 3) == 0 &&
+                     (as0 & 3) == 0 && ((uintptr_t)A & 15) == 0;
+  const int mode = (h_vec && as2 == 1 && (as1 & 3) == 0)   ? kCopyRowVec
+                   : (h_vec && as1 == 1 && (as2 & 3) == 0) ? kCopyColVec
+                                                           : kCopyScalar;
   // the batch goes to grid.y: at most kMaxGridY matrices per launch
   for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
     const int64_t nb = (batch - b0 < kMaxGridY) ? batch - b0 : kMaxGridY;
     hipLaunchKernelGGL(copy_to_colmajor_kernel, dim3(ntile * ntj, (unsigned)nb), dim3(256), 0, stream, A + b0 * as0,
-                       as0, as1, as2, H + b0 * hs0, hs0, ldh, n, ntile, tj0, vec);
+                       as0, as1, as2, H + b0 * hs0, hs0, ldh, n, ntile, tj0, mode);
     const hipError_t e = hipGetLastError();
     if (e != hipSuccess) return e;
   }

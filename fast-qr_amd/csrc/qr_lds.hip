@@ -194,7 +194,6 @@ __global__ void __launch_bounds__(kLdsWaves * 64) qr_lds_kernel(const float* __r
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
   const int lane = tid & 63;
-  const int h = lane >> 5, l32 = lane & 31;
   const int ldm = lds_ld(n);
   const int npad = (n + 3) & ~3;
 
@@ -203,7 +202,30 @@ __global__ void __launch_bounds__(kLdsWaves * 64) qr_lds_kernel(const float* __r
   // LDS store is one 16-byte column segment (the bank pattern of an MFMA tile
   // load); 16 rows per wave and pass keep 48 loads in flight per lane.
   const float* Ab = A + b * as0;
-  for (int r0 = 16 * wave; r0 < npad; r0 += 16 * kLdsWaves) {
+  const bool a_vec = as1 == 1 && (as2 & 3) == 0 && (as0 & 3) == 0 && ((uintptr_t)A & 15) == 0;
+  if (a_vec) {
+    // column-major source: a wave reads whole columns, lanes taking four
+    // consecutive rows each (16-byte global loads and LDS stores); eight
+    // columns per wave and pass keep eight loads in flight per lane
+    const int r = 4 * lane;
+    for (int c0 = 8 * wave; c0 < n; c0 += 8 * kLdsWaves) {
+      f32x4 v[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        const int c = c0 + j;
+        if (c < n && r + 3 < n) {
+          v[j] = *reinterpret_cast<const f32x4*>(Ab + (int64_t)c * as2 + r);
+        } else {
+#pragma unroll
+          for (int i = 0; i < 4; ++i) v[j][i] = (c < n && r + i < n) ? Ab[(int64_t)c * as2 + r + i] : 0.0f;
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j)
+        if (c0 + j < n && r < npad) *reinterpret_cast<f32x4*>(M + (c0 + j) * ldm + r) = v[j];
+    }
+  }
+  for (int r0 = 16 * wave; !a_vec && r0 < npad; r0 += 16 * kLdsWaves) {
     f32x4 v[kLdsMaxTiles / 2][4];
 #pragma unroll
     for (int cc = 0; cc < kLdsMaxTiles / 2; ++cc) {

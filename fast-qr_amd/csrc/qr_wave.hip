@@ -203,15 +203,24 @@ __global__ void __launch_bounds__(64) qr_wave_kernel(const float* __restrict__ A
   q.kq = lane >> 4;
   q.cn = lane & 15;
   const float* Ab = A + b * as0;
+  // Column-major source with 16-byte aligned columns: a lane's four rows of a
+  // column are one 16-byte load (four lanes cover 64 contiguous bytes of each
+  // column).  Otherwise one element per load, lanes along the columns of a row.
+  const bool a_vec = as1 == 1 && (as2 & 3) == 0 && (as0 & 3) == 0 && ((uintptr_t)A & 15) == 0;
 #pragma unroll
   for (int tr = 0; tr < NT; ++tr) {
 #pragma unroll
     for (int tc = 0; tc < NT; ++tc) {
       const int c = 16 * tc + q.cn;
+      const int r0 = 16 * tr + 4 * q.kq;
+      if (a_vec && c < n && r0 + 3 < n) {
+        q.X[tr][tc] = *reinterpret_cast<const f32x4*>(Ab + c * as2 + r0);
+      } else {
 #pragma unroll
-      for (int i = 0; i < 4; ++i) {
-        const int r = 16 * tr + 4 * q.kq + i;
-        q.X[tr][tc][i] = (r < n && c < n) ? Ab[r * as1 + c * as2] : 0.0f;
+        for (int i = 0; i < 4; ++i) {
+          const int r = r0 + i;
+          q.X[tr][tc][i] = (r < n && c < n) ? Ab[r * as1 + c * as2] : 0.0f;
+        }
       }
     }
     q.tv[tr] = 0.0f;

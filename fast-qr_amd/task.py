@@ -1,5 +1,14 @@
-"""Interface types of the submission entry point (official/task.py:4-13)."""
-from typing import NotRequired, TypedDict, TypeVar
+"""Interface types of the submission entry point (official/task.py:4-13).
+
+``NotRequired`` is in ``typing`` from Python 3.11; on older interpreters it
+and a ``TypedDict`` that understands it come from ``typing_extensions``.
+"""
+from typing import TypeVar
+
+try:
+    from typing import NotRequired, TypedDict
+except ImportError:  # Python < 3.11
+    from typing_extensions import NotRequired, TypedDict
 
 import torch
 

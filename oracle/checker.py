@@ -19,7 +19,8 @@ Two families of gates:
      ||Q^T Q - I||_F       <= 1e-5 * n
      |R_ii| and tau agree with CPU geqrf to 1e-4 relative (same sign of R_ii),
      compared on the columns whose |R_ii| lies above the rounding floor
-     4 * sqrt(n) * eps32 * ||A||_2 / 1e-4 (see ``rdiag_tau_agreement``).
+     2 * sqrt(n) * eps32 * ||A||_2 / 1e-4 and whose fp32 reference is itself
+     determined (see ``rdiag_tau_agreement``).
 """
 from __future__ import annotations
 
@@ -145,11 +146,25 @@ class AgreementReport:
     compared: int
     masked: int
     limit: float
+    compared_per_matrix: list = field(default_factory=list)
+    sign_flips: int = 0  # columns whose undetermined sign (alpha ~ 0) came out the other way
+    r_only: int = 0  # compared columns after such a flip (|R_ii| compared, tau not)
+
+    def compared_fraction(self, members=None) -> float:
+        """Fraction of columns above the floor, over all matrices or `members`."""
+        per = self.compared_per_matrix
+        idx = range(len(per)) if members is None else members
+        cols = (self.compared + self.masked) // max(len(per), 1)
+        tot = sum(per[i] for i in idx)
+        return tot / max(cols * len(list(idx)), 1)
 
     def message(self) -> str:
+        flips = (f", {self.sign_flips} undetermined sign(s) taken the other way ({self.r_only} later columns "
+                 f"compared by |R_ii| only)" if self.sign_flips else "")
         return (
             f"|R_ii| rel max={self.rdiag_rel_max:.3e}, tau rel max={self.tau_rel_max:.3e} "
             f"(limit {self.limit:.0e}) over {self.compared} columns, {self.masked} below the rounding floor"
+            + flips
         )
 
 
@@ -168,19 +183,57 @@ def norm2_estimate(a: torch.Tensor, iters: int = 30) -> torch.Tensor:
     return est
 
 
-def rdiag_tau_agreement(a, h, tau, h_ref, tau_ref, rtol: float = 1e-4, floor_factor: float = 4.0
-                        ) -> AgreementReport:
+# Calibration of the floor (MKL fp32 geqrf against MKL fp64 geqrf, and the HIP
+# path against both, on the benchmark inputs -- Gaussian n = 32..4096 and every
+# structured family of the 640 x 512 and 60 x 1024 workloads -- and on the
+# task's 22 test and 12 benchmark cases).  Above floor_factor = 1 one fp32 code
+# stays within 3.0e-5 of fp64 on the benchmark inputs (clustered spectrum;
+# Gaussian 1.9e-5), but the last columns of the banded test case reach 6.1e-4
+# (MKL) and 1.2e-4 (HIP path, where MKL happens to be within 8e-6): their R_ii
+# carry the rounding of every earlier step, about n eps32 ||A|| rather than
+# sqrt(n) eps32 ||A||.  Hence floor_factor = 2 (the banded case's worst
+# compared column then differs by 4.9e-5), and a column is compared only where
+# the fp32 reference is itself determined to a quarter of the tolerance (fp32
+# geqrf within DETERMINACY * rtol of fp64 geqrf on the same input).
+DEFAULT_FLOOR_FACTOR = 2.0
+DETERMINACY = 0.25
+# alpha / beta below this many sqrt(n) eps32 has a sign set by rounding
+SIGN_TOL_FACTOR = 8.0
+
+# Minimum fraction of columns compared per structure family at these settings
+# (observed on the benchmark workloads in brackets): Gaussian [1.000 at n = 32,
+# 0.994 at 176, 0.991 at 352, 0.988 at 512, 0.977 at 1024, 0.955 at 2048,
+# 0.910 at 4096]; the rank-deficient and clustered spectra compare their
+# leading half [0.497], near-rank inputs their leading n - 256 columns [0.748
+# at n = 1024].
+MIN_COMPARED_FRACTION = {"dense": {32: 0.97, 176: 0.98, 352: 0.98, 512: 0.975, 1024: 0.96, 2048: 0.93, 4096: 0.88},
+                         "rankdef": 0.45, "clustered": 0.45, "nearrank": 0.70}
+
+
+def min_compared_fraction(family: str, n: int):
+    """Expected minimum compared fraction for a family at size n, or None."""
+    v = MIN_COMPARED_FRACTION.get(family)
+    if isinstance(v, dict):
+        return v.get(n)
+    return v
+
+
+def rdiag_tau_agreement(a, h, tau, h_ref, tau_ref, rtol: float = 1e-4,
+                        floor_factor: float = DEFAULT_FLOOR_FACTOR,
+                        determinacy: float | None = DETERMINACY) -> AgreementReport:
     """Compare |R_ii| and tau with a reference factorisation (CPU geqrf).
 
     Column i of matrix b is compared when
         |R_ii(ref)| > floor_factor * sqrt(n) * eps32 * ||A_b||_2 / rtol,
-    i.e. where the expected rounding spread between two correct fp32
-    Householder codes (about sqrt(n) * eps32 * ||A||_2 in absolute terms,
-    measured MKL-fp32 vs MKL-fp64 and oracle vs MKL on the benchmark inputs)
-    is below rtol * |R_ii| by the safety factor.  Below that floor the R_ii of
-    rank-deficient, clustered and near-rank inputs are rounding noise and their
-    tau is arbitrary in [1, 2]; those columns are counted, not compared.  On
-    compared columns the sign of R_ii must match (same LAPACK convention).
+    i.e. where the rounding spread between two correct fp32 Householder codes
+    (about sqrt(n) * eps32 * ||A||_2 in absolute terms) stays below rtol *
+    |R_ii| (calibration above), and, with ``determinacy``, where the fp32
+    reference agrees with fp64 geqrf of the same input to determinacy * rtol
+    (its |R_ii| and tau are then fixed by the input, not by rounding).  Below
+    the floor the R_ii of rank-deficient, clustered and near-rank inputs are
+    rounding noise and their tau is arbitrary in [1, 2]; those columns are
+    counted, not compared.  On compared columns the sign of R_ii must match
+    (same LAPACK convention).
     """
     a = _t(a).double()
     h = _t(h).double()
@@ -193,10 +246,28 @@ def rdiag_tau_agreement(a, h, tau, h_ref, tau_ref, rtol: float = 1e-4, floor_fac
     a2 = norm2_estimate(a).reshape(batch, 1)
     floor = floor_factor * math.sqrt(max(n, 1)) * EPS32 * a2 / rtol
     mask = dr.abs() > floor
+    h64, t64 = torch.geqrf(a)
+    if determinacy is not None:
+        d64 = torch.diagonal(h64, dim1=-2, dim2=-1).abs()
+        fixed_r = (dr.abs() - d64).abs() <= determinacy * rtol * d64
+        fixed_t = (tau_ref - t64).abs() <= determinacy * rtol * t64.abs()
+        mask = mask & fixed_r & fixed_t
+    # Undetermined signs: where alpha / beta = 1 - tau is below the rounding
+    # level of alpha (SIGN_TOL_FACTOR sqrt(n) eps32, from fp64 geqrf), the
+    # sign of alpha -- hence of beta = R_kk -- is decided by rounding, and a
+    # correct fp32 code may pick either.  After such a column k picks the other
+    # sign the factorisations go different ways: every later |R_jj| is still
+    # the same (R is unique up to the signs of its rows), but the later tau and
+    # reflectors are not.  Columns from k on keep the |R_jj| comparison only.
+    undetermined = (1.0 - t64).abs() <= SIGN_TOL_FACTOR * math.sqrt(max(n, 1)) * EPS32
+    flipped = undetermined & (torch.sign(d) != torch.sign(dr))
+    after = torch.cumsum(flipped.to(torch.int64), dim=-1) > 0  # from the first flip on
     rel_r = (d.abs() - dr.abs()).abs() / dr.abs().clamp_min(1e-300)
     rel_t = (tau - tau_ref).abs() / tau_ref.abs().clamp_min(1e-300)
-    sign_ok = bool(((torch.sign(d) == torch.sign(dr)) | ~mask).all())
+    sign_ok = bool(((torch.sign(d) == torch.sign(dr)) | ~mask | after).all())
+    tmask = mask & ~after
     rmax = float(torch.where(mask, rel_r, torch.zeros_like(rel_r)).max()) if mask.any() else 0.0
-    tmax = float(torch.where(mask, rel_t, torch.zeros_like(rel_t)).max()) if mask.any() else 0.0
+    tmax = float(torch.where(tmask, rel_t, torch.zeros_like(rel_t)).max()) if tmask.any() else 0.0
     ok = sign_ok and rmax <= rtol and tmax <= rtol
-    return AgreementReport(ok, rmax, tmax, int(mask.sum()), int((~mask).sum()), rtol)
+    return AgreementReport(ok, rmax, tmax, int(mask.sum()), int((~mask).sum()), rtol, mask.sum(dim=-1).tolist(),
+                           int(flipped.sum()), int((mask & after).sum()))

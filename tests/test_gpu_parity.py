@@ -123,13 +123,16 @@ def test_zero_matrix(cuda, n):
     assert torch.equal(h, a)
 
 
-@pytest.mark.parametrize("n", [32, 176])
+@pytest.mark.parametrize("n", [5, 32, 63, 101, 176])
 def test_column_major_and_strided_inputs(cuda, n):
+    # the wave64 and LDS-resident kernels load column-major A in 16-byte column
+    # segments (n a multiple of 4), element by element otherwise
     _say(f"[strides] n={n}")
     a = gaussian(4, n, 400 + n)
     h_ref, tau_ref = run_gpu(a, cuda)
     a_cm = a.transpose(1, 2).contiguous().transpose(1, 2)  # column-major view, same values
     h2, tau2 = run_gpu(a_cm, cuda)
+    assert_parity(a, h2, tau2)
     assert torch.equal(h2, h_ref) and torch.equal(tau2, tau_ref)
     big = torch.zeros((8, n + 3, n + 5))
     big[::2, 1 : n + 1, 2 : n + 2] = a
@@ -137,6 +140,48 @@ def test_column_major_and_strided_inputs(cuda, n):
     h3, tau3 = custom_kernel(view)
     torch.cuda.synchronize()
     assert torch.equal(h3.cpu(), h_ref) and torch.equal(tau3.cpu(), tau_ref)
+
+
+# Column-major input (BASELINE C2 names that layout) and generic strides on
+# the blocked path: the copy into H takes 16-byte column segments (column-major,
+# n a multiple of 4), element loads (odd n, or any other strides); both are
+# checked against the oracle and against the row-major run, which must be
+# bit-identical (the same H bytes enter the same kernels).
+@pytest.mark.parametrize("batch,n", [(40, 352), (6, 512), (2, 1025), (2, 2049), (3, 178)])
+def test_blocked_path_column_major_input(cuda, batch, n):
+    _say(f"[column-major] batch={batch} n={n}")
+    a = gaussian(batch, n, 800 + n)
+    h_rm, t_rm = run_gpu(a, cuda)
+    a_cm = a.transpose(1, 2).contiguous().transpose(1, 2)  # column-major, same values
+    assert a_cm.stride() == (n * n, 1, n)
+    h, tau = run_gpu(a_cm, cuda)
+    ag = assert_parity(a, h, tau)
+    assert torch.equal(h, h_rm) and torch.equal(tau, t_rm)
+    _say(f"  {ag.message()}")
+
+
+@pytest.mark.parametrize("n", [352, 600])
+def test_blocked_path_generic_strides(cuda, n):
+    # a padded column-major batch (16-byte column segments), and every other
+    # row of a taller batch (element loads)
+    _say(f"[strided blocked] n={n}")
+    a = gaussian(3, n, 900 + n)
+    h_rm, t_rm = run_gpu(a, cuda)
+    store = torch.zeros((3, n + 8, n + 4))
+    store[:, 3 : n + 3, 4 : n + 4] = a.transpose(1, 2)
+    # column-major, leading dimension n + 4, 16-byte aligned columns
+    view = store.to(cuda)[:, 3 : n + 3, 4 : n + 4].transpose(1, 2)
+    assert view.stride() == ((n + 8) * (n + 4), 1, n + 4)
+    h, tau = custom_kernel(view)
+    torch.cuda.synchronize()
+    assert torch.equal(h.cpu(), h_rm) and torch.equal(tau.cpu(), t_rm)
+    every_other = torch.zeros((3, 2 * n, n))
+    every_other[:, ::2, :] = a
+    view2 = every_other.to(cuda)[:, ::2, :]  # row stride 2n
+    h2, tau2 = custom_kernel(view2)
+    torch.cuda.synchronize()
+    assert torch.equal(h2.cpu(), h_rm) and torch.equal(tau2.cpu(), t_rm)
+    assert_parity(a, h_rm, t_rm)
 
 
 def test_deterministic_rerun_is_bitwise_identical(cuda):
@@ -159,26 +204,47 @@ def test_input_is_not_written(cuda):
     assert torch.equal(a, before)
 
 
-WORKLOAD_CASES = [
-    ("C1", 0, None),
-    ("C2", 0, None),
-    ("C2", 1, None),
-    ("C3", 0, 24),
-    ("C4", 0, 8),
-    ("C5", 0, 2),
-    ("C5", 1, 1),
-]
+def stratified_sample(labels, per_family=3):
+    """Matrix indices to check in a large batch: the first and last matrix,
+    both sides of the first and last 8-matrix boundary (workgroups are spread
+    over the 8 XCDs by matrix), and `per_family` matrices of every structure
+    family spread over its members."""
+    batch = len(labels)
+    idx = {0, batch - 1, min(7, batch - 1), min(8, batch - 1), max(batch - 9, 0), max(batch - 8, 0)}
+    for fam in sorted(set(labels)):
+        members = [i for i, lab in enumerate(labels) if lab == fam]
+        k = min(per_family, len(members))
+        idx.update(members[(j * (len(members) - 1)) // max(k - 1, 1)] for j in range(k))
+    return sorted(idx)
 
 
-@pytest.mark.parametrize("name,idx,limit", WORKLOAD_CASES)
-def test_benchmark_workloads_match_geqrf(cuda, name, idx, limit):
+WORKLOAD_CASES = [("C1", 0), ("C2", 0), ("C2", 1), ("C3", 0), ("C4", 0), ("C5", 0), ("C5", 1)]
+
+
+@pytest.mark.parametrize("name,idx", WORKLOAD_CASES)
+def test_benchmark_workloads_match_geqrf(cuda, name, idx):
+    # the whole configured batch goes through custom_kernel (the schedule the
+    # bench times); the oracle checks a stratified sample of it (every matrix
+    # for n <= 352)
     shape = inputs.WORKLOADS[name][idx]
-    _say(f"[workload] {name} {shape.label} first {limit or shape.batch}")
     a = inputs.generate(shape)
-    if limit is not None:
-        a = a[:limit].contiguous()
-    h, tau = run_gpu(a, cuda)
-    ag = assert_parity(a, h, tau)
+    labels = inputs.structure_labels(shape)
+    sample = list(range(shape.batch)) if shape.n <= 352 else stratified_sample(labels)
+    _say(f"[workload] {name} {shape.label}: full batch, checking {len(sample)} matrices {sample}")
+    d = a.to(cuda)
+    h, tau = custom_kernel(d)
+    torch.cuda.synchronize()
+    sel = torch.tensor(sample)
+    a_s, h_s, t_s = a[sel], h[sel.to(cuda)].cpu(), tau[sel.to(cuda)].cpu()
+    del d, h, tau
+    ag = assert_parity(a_s, h_s, t_s)
+    # the agreement must cover what the floor calibration promises per family
+    fams = [labels[i] for i in sample]
+    for fam in sorted(set(fams)):
+        want = checker.min_compared_fraction(fam, shape.n)
+        got = ag.compared_fraction([j for j, f in enumerate(fams) if f == fam])
+        _say(f"  {fam}: {got:.3f} of the columns compared (minimum {want})")
+        assert want is not None and got >= want, f"{fam}: only {got:.3f} of the columns above the rounding floor"
     _say(f"  {ag.message()}")
 
 

@@ -189,6 +189,72 @@ def test_checker_rejects_bad_outputs():
     assert not checker.official_check(a, h2, tau)[0]
 
 
+def test_norm2_estimate_is_a_tight_lower_bound():
+    # power iteration on A^T A approaches ||A||_2 from below: never above it,
+    # within 3% after its 30 steps; exact for a rank-one matrix and for
+    # U diag(s) V^T with a clear gap (||A||_2 = s_1)
+    from fastqr import inputs
+
+    gen = torch.Generator().manual_seed(11)
+    mats = [torch.randn((3, 64, 64), generator=gen, dtype=torch.float64),
+            torch.randn((2, 512, 512), generator=gen, dtype=torch.float64)]
+    u = torch.randn((2, 40, 1), generator=gen, dtype=torch.float64)
+    mats.append(u @ u.transpose(-1, -2))
+    s = torch.linspace(1.0, 0.1, 96, dtype=torch.float64)
+    s[0] = 7.0
+    g32 = torch.Generator().manual_seed(12)
+    mats.append(inputs.svd_structured(96, s, g32, 2).double())
+    for a in mats:
+        est = checker.norm2_estimate(a)
+        true = torch.linalg.matrix_norm(a, ord=2)
+        assert bool((est <= true * (1 + 1e-9)).all()), (est, true)
+        assert bool((est >= 0.97 * true).all()), (est, true)
+    assert torch.allclose(checker.norm2_estimate(mats[2]), torch.linalg.matrix_norm(mats[2], ord=2), rtol=1e-12)
+    assert torch.allclose(checker.norm2_estimate(mats[3]), torch.full((2,), 7.0, dtype=torch.float64), rtol=1e-5)
+
+
+def _other_sign_factorisation(a):
+    """A valid Householder QR of one fp64 matrix that takes the other sign of
+    beta in column 0 (beta = +sign(alpha) ||x||), then LAPACK geqrf on the
+    trailing block: what a correct code produces when alpha ~ 0 rounds the
+    other way."""
+    n = a.shape[-1]
+    x = a[:, 0].clone()
+    alpha, sigma = x[0].item(), float((x[1:] ** 2).sum())
+    beta = math.copysign(math.sqrt(alpha * alpha + sigma), alpha)  # LAPACK: -sign(alpha) ||x||
+    tau0 = (beta - alpha) / beta
+    v = x / (alpha - beta)
+    v[0] = 1.0
+    b = a - tau0 * torch.outer(v, v @ a)
+    h2, t2 = torch.geqrf(b[1:, 1:])
+    h = b.clone()
+    h[1:, 0] = v[1:]
+    h[0, 0] = beta
+    h[1:, 1:] = h2
+    tau = torch.cat([torch.tensor([tau0], dtype=a.dtype), t2])
+    return h, tau
+
+
+@pytest.mark.parametrize("ratio,flip_allowed", [(1e-9, True), (0.3, False)])
+def test_undetermined_sign_is_accepted_only_where_alpha_vanishes(ratio, flip_allowed):
+    # column 0 with alpha / ||x|| = ratio: at 1e-9 its sign is rounding noise
+    # and the other-sign factorisation must pass (later columns compared by
+    # |R_jj| only); at 0.3 the sign is determined and the same construction
+    # is a planted mistake the agreement must catch
+    g = torch.Generator().manual_seed(21)
+    a = torch.randn((8, 8), generator=g, dtype=torch.float64)
+    a[0, 0] = ratio * torch.linalg.vector_norm(a[1:, 0])
+    h_alt, t_alt = _other_sign_factorisation(a)
+    q = torch.linalg.householder_product(h_alt, t_alt)
+    assert torch.allclose(q @ torch.triu(h_alt), a, atol=1e-12)  # a valid QR of A
+    a32 = a.float().unsqueeze(0)
+    h_ref, t_ref = torch.geqrf(a32)
+    rep = checker.rdiag_tau_agreement(a32, h_alt.float().unsqueeze(0), t_alt.float().unsqueeze(0), h_ref, t_ref)
+    assert rep.ok == flip_allowed, rep.message()
+    if flip_allowed:
+        assert rep.sign_flips == 1 and rep.r_only >= 6
+
+
 def test_agreement_floor_masks_rank_deficient_tail_only():
     g = load("rankdef_4x8")
     rep = checker.rdiag_tau_agreement(g["a"], g["h_scipy"], g["tau_scipy"], g["h"], g["tau"])
