@@ -10,6 +10,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <atomic>
 #include <vector>
 
 #include "../../include/fastqr.h"
@@ -41,6 +42,9 @@ constexpr int kWaveMaxN = 64;
 constexpr int64_t kRowSplitMinN = 2049;
 
 bool use_rowsplit(int64_t /*batch*/, int64_t n) { return n >= kRowSplitMinN; }
+
+// Panel groups per factorisation: at least 64 columns each, n <= kMaxN.
+constexpr int kMaxGroups = (int)(kMaxN / 64);
 
 // Strip-resident path, small batches of tall matrices (8 x 2048): the narrow
 // update after a 32-column panel taller than kWyrNarrowMinRows runs on the
@@ -168,29 +172,36 @@ hipError_t timed(int kind, double flops, double bytes, hipStream_t stream, F&& f
 // overlapping the next group's panels.  Two scratch areas (one per stream) and
 // two banks of T slots and group T alternate by group parity.
 int run_rowsplit(float* H, int64_t batch, int64_t hs0, int64_t ldh, float* tau, int64_t ts0, int64_t ts1, float* Tws,
-                 int n, bool vec, hipStream_t stream) {
+                 int n, bool vec, bool single_stream, hipStream_t stream) {
   using fastqr::WyrCall;
   const int64_t slot_floats = batch * fastqr::kMaxSlots * 1024;
   float* Tg0 = Tws + slot_floats;
+  // one scratch area per stream (a single stream needs one)
   float* area[2] = {Tg0 + 2 * batch * fastqr::kWyrTgStride, nullptr};
-  area[1] = area[0] + fastqr::wyr_workspace_floats(batch, n);
+  area[1] = single_stream ? area[0] : area[0] + fastqr::wyr_workspace_floats(batch, n);
   const double bd = (double)batch;
 
   struct Group {
     int g0, nb, g_end, npan, slot_base;
   };
-  std::vector<Group> groups;
-  for (int g0 = 0, gi = 0; g0 < n; ++gi) {
+  Group groups[kMaxGroups];
+  int ngroups = 0;
+  for (int g0 = 0; g0 < n; ++ngroups) {
     const int nb = fastqr::panel_width_for(n - g0);
     const int span = fastqr::kMaxWY * nb < fastqr::kWyrMaxK ? fastqr::kMaxWY * nb : fastqr::kWyrMaxK;
     const int g_end = (g0 + span < n) ? g0 + span : n;
-    groups.push_back(Group{g0, nb, g_end, (g_end - g0 + nb - 1) / nb, (gi & 1) * fastqr::kMaxWY});
+    if (ngroups == kMaxGroups) return fail(FASTQR_EINVAL, "too many panel groups for n=%d", n);
+    groups[ngroups] = Group{g0, nb, g_end, (g_end - g0 + nb - 1) / nb, (ngroups & 1) * fastqr::kMaxWY};
     g0 = g_end;
   }
-  DeviceAux* aux = device_aux();
-  if (!aux) return fail(FASTQR_EINVAL, "cannot create the side stream");
-  const hipStream_t side = aux->side;
+  // Single stream: the side stream's work (panels, narrow and look-ahead
+  // updates) is issued on the caller's stream in the same order, so each
+  // group's wide update simply runs before the next group's panels.
+  DeviceAux* aux = single_stream ? nullptr : device_aux();
+  if (!single_stream && !aux) return fail(FASTQR_EINVAL, "cannot create the side stream");
+  const hipStream_t side = single_stream ? stream : aux->side;
   auto join = [&](hipStream_t waiter, hipStream_t signaller) -> hipError_t {
+    if (single_stream) return hipSuccess;
     hipEvent_t ev = aux->take();
     if (!ev) return hipErrorOutOfMemory;
     hipError_t e = hipEventRecord(ev, signaller);
@@ -223,8 +234,8 @@ int run_rowsplit(float* H, int64_t batch, int64_t hs0, int64_t ldh, float* tau, 
 
   hipError_t e = join(side, stream);  // the side stream starts after the copy
   if (e != hipSuccess) return hip_fail(e, "stream join");
-  std::vector<bool> rest_done(groups.size(), false);
-  for (size_t gi = 0; gi < groups.size(); ++gi) {
+  bool rest_done[kMaxGroups] = {};
+  for (int gi = 0; gi < ngroups; ++gi) {
     const Group& G = groups[gi];
     for (int i = 0; i < G.npan; ++i) {
       const int pk = G.g0 + i * G.nb;
@@ -242,7 +253,7 @@ int run_rowsplit(float* H, int64_t batch, int64_t hs0, int64_t ldh, float* tau, 
         if ((e = run_wyr(c, side)) != hipSuccess) return hip_fail(e, "narrow update launch");
       }
     }
-    if (gi + 1 == groups.size()) break;
+    if (gi + 1 == ngroups) break;
     const Group& Nx = groups[gi + 1];
     float* Tg = Tg0 + (int64_t)(gi & 1) * batch * fastqr::kWyrTgStride;
     // the next group's columns last received the previous group's wide update
@@ -268,125 +279,25 @@ int run_rowsplit(float* H, int64_t batch, int64_t hs0, int64_t ldh, float* tau, 
   if ((e = join(stream, side)) != hipSuccess) return hip_fail(e, "stream join");
   return FASTQR_OK;
 }
-}  // namespace
 
-extern "C" {
-
-int fastqr_profile_enable(int on) {
-  if (on) {
-    (void)g_prof.drain();
-    for (Totals& t : g_prof.totals) t = Totals{};
-  }
-  g_prof.on = on != 0;
-  return FASTQR_OK;
-}
-
-int fastqr_profile_collect(int kind, int64_t* launches, double* milliseconds, double* flops, double* bytes) {
-  if (kind < 0 || kind >= FASTQR_PROFILE_KINDS) return fail(FASTQR_EINVAL, "profile kind %d out of range", kind);
-  const hipError_t e = g_prof.drain();
-  const Totals& t = g_prof.totals[kind];
-  if (launches) *launches = t.launches;
-  if (milliseconds) *milliseconds = t.ms;
-  if (flops) *flops = t.flops;
-  if (bytes) *bytes = t.bytes;
-  return e == hipSuccess ? FASTQR_OK : hip_fail(e, "profile collect");
-}
-
-const char* fastqr_profile_kind_name(int kind) {
-  return (kind >= 0 && kind < FASTQR_PROFILE_KINDS) ? kKindNames[kind] : "";
-}
-
-int fastqr_version(void) { return 1; }
-
-const char* fastqr_last_error(void) { return g_last_error; }
-
-void fastqr_debug_force_error(int code) { g_forced_error = code; }
-
-const char* fastqr_path_name(int64_t n) {
-  if (n <= kWaveMaxN) return "wave64";
-  if (n <= fastqr::kLdsMaxN) return "lds";
-  return "blocked";
-}
-
-size_t fastqr_workspace_bytes(int64_t batch, int64_t n) {
+// Workspace of the blocked path: the T slots; for tall matrices (row-split
+// update) two group-T banks and the partial products of each stream.
+size_t workspace_bytes_for(int64_t batch, int64_t n, bool single_stream) {
   if (batch <= 0 || n <= fastqr::kLdsMaxN || n > kMaxN) return 0;
   size_t floats = (size_t)batch * fastqr::kMaxSlots * 32 * 32;
   if (use_rowsplit(batch, n))
-    floats += 2 * (size_t)batch * fastqr::kWyrTgStride + 2 * fastqr::wyr_workspace_floats(batch, (int)n);
+    floats += 2 * (size_t)batch * fastqr::kWyrTgStride +
+              (single_stream ? 1 : 2) * fastqr::wyr_workspace_floats(batch, (int)n);
   else if (use_wyr_narrow(batch, n))
     floats += fastqr::wyr_workspace_floats(batch, (int)n);
   return (floats * sizeof(float) + 255) & ~(size_t)255;
 }
 
-size_t fastqr_orgqr_workspace_bytes(int64_t batch, int64_t n) {
-  if (batch <= 0 || n <= 0 || n > kMaxN) return 0;
-  // the batch is processed in chunks of at most kMaxGridY matrices
-  const int64_t chunk = batch < fastqr::kMaxGridY ? batch : fastqr::kMaxGridY;
-  return (fastqr::orgqr_workspace_floats(chunk, (int)n) * sizeof(float) + 255) & ~(size_t)255;
-}
-
-int fastqr_orgqr_f32(const float* H, int64_t batch, int64_t n, int64_t h_s0, int64_t h_s1, int64_t h_s2,
-                     const float* tau, int64_t tau_s0, int64_t tau_s1, float* Q, int64_t q_s0, int64_t q_s1,
-                     int64_t q_s2, void* workspace, size_t workspace_bytes, void* stream_ptr) {
-  g_last_error[0] = '\0';
-  if (g_forced_error != 0) {
-    const int code = g_forced_error;
-    g_forced_error = 0;
-    return fail(code, "forced error %d (test hook)", code);
-  }
-  if (batch < 0 || n < 0) return fail(FASTQR_EINVAL, "batch and n must be non-negative (got %lld, %lld)",
-                                      (long long)batch, (long long)n);
-  if (batch == 0 || n == 0) return FASTQR_OK;
-  if (n > kMaxN) return fail(FASTQR_EINVAL, "n=%lld exceeds the supported maximum %lld", (long long)n,
-                             (long long)kMaxN);
-  if (batch > 2147483647LL) return fail(FASTQR_EINVAL, "batch too large");
-  if (!H || !tau || !Q) return fail(FASTQR_EINVAL, "H, tau and Q must be non-null device pointers");
-  if (h_s0 < 0 || h_s1 < 0 || h_s2 < 0 || q_s0 < 0 || q_s2 < 0 || tau_s0 < 0 || tau_s1 < 0)
-    return fail(FASTQR_EINVAL, "negative strides are not supported");
-  if (batch > 1 && (q_s0 == 0 || tau_s0 == 0))
-    return fail(FASTQR_EINVAL, "Q and tau batch strides must be non-zero when batch > 1");
-  if (n > 1 && (tau_s1 == 0 || h_s1 == 0 || h_s2 == 0)) return fail(FASTQR_EINVAL, "H and tau strides must be non-zero");
-  if (q_s1 != 1 || q_s2 < n)
-    return fail(FASTQR_ELAYOUT, "Q must have contiguous columns (stride (*, 1, >=n)); got (%lld, %lld, %lld)",
-                (long long)q_s0, (long long)q_s1, (long long)q_s2);
-  if (q_s2 * n * 4 >= (int64_t)1 << 31)
-    return fail(FASTQR_ELAYOUT, "one matrix of Q spans %lld bytes; at most 2 GiB are addressed",
-                (long long)(q_s2 * n * 4));
-  if (batch > 1 && q_s0 < q_s2 * n)
-    return fail(FASTQR_ELAYOUT, "Q batch stride %lld smaller than one matrix (%lld)", (long long)q_s0,
-                (long long)(q_s2 * n));
-  const size_t need = fastqr_orgqr_workspace_bytes(batch, n);
-  if (workspace_bytes < need || (need > 0 && workspace == nullptr))
-    return fail(FASTQR_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
-  if (((uintptr_t)workspace & 15) != 0) return fail(FASTQR_EWORKSPACE, "workspace must be 16-byte aligned");
-  const bool same = ((const float*)Q == H && q_s0 == h_s0 && q_s1 == h_s1 && q_s2 == h_s2);
-  const int64_t q_span = span_elems(batch, n, q_s0, 1, q_s2);
-  if (!same && ranges_overlap(H, span_elems(batch, n, h_s0, h_s1, h_s2), Q, q_span))
-    return fail(FASTQR_EOVERLAP, "H and Q overlap with different layouts");
-  if (ranges_overlap(tau, span_elems(batch, n, tau_s0, tau_s1, 0), Q, q_span))
-    return fail(FASTQR_EOVERLAP, "tau and Q overlap");
-  const bool vec = ((uintptr_t)Q % 16 == 0) && (q_s0 % 4 == 0) && (q_s2 % 4 == 0) && (n % 4 == 0);
-  // chunks of at most kMaxGridY matrices (its kernels put the batch in grid.y),
-  // one after another on the stream, sharing the workspace
-  for (int64_t b0 = 0; b0 < batch; b0 += fastqr::kMaxGridY) {
-    const int64_t nb = (batch - b0 < fastqr::kMaxGridY) ? batch - b0 : fastqr::kMaxGridY;
-    const hipError_t e = fastqr::launch_orgqr(H + b0 * h_s0, nb, (int)n, h_s0, h_s1, h_s2, tau + b0 * tau_s0, tau_s0,
-                                              tau_s1, Q + b0 * q_s0, q_s0, q_s2, (float*)workspace, vec,
-                                              (hipStream_t)stream_ptr);
-    if (e != hipSuccess) return hip_fail(e, "orgqr launch");
-  }
-  return FASTQR_OK;
-}
-
-int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a_s1, int64_t a_s2,
-                     float* H, int64_t h_s0, int64_t h_s1, int64_t h_s2, float* tau, int64_t tau_s0,
-                     int64_t tau_s1, void* workspace, size_t workspace_bytes, void* stream_ptr) {
-  g_last_error[0] = '\0';
-  if (g_forced_error != 0) {
-    const int code = g_forced_error;
-    g_forced_error = 0;
-    return fail(code, "forced error %d (test hook)", code);
-  }
+// fastqr_geqrf_f32 after the test hook.  `single_stream` keeps every launch
+// on the caller's stream (no side stream, no events: nothing is created).
+int geqrf_impl(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a_s1, int64_t a_s2, float* H,
+               int64_t h_s0, int64_t h_s1, int64_t h_s2, float* tau, int64_t tau_s0, int64_t tau_s1, void* workspace,
+               size_t workspace_bytes, bool single_stream, void* stream_ptr) {
   if (batch < 0 || n < 0) return fail(FASTQR_EINVAL, "batch and n must be non-negative (got %lld, %lld)",
                                       (long long)batch, (long long)n);
   if (batch == 0 || n == 0) return FASTQR_OK;
@@ -434,7 +345,7 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   if (batch > 1 && h_s0 < h_s2 * n)
     return fail(FASTQR_ELAYOUT, "H batch stride %lld smaller than one matrix (%lld)", (long long)h_s0,
                 (long long)(h_s2 * n));
-  const size_t need = fastqr_workspace_bytes(batch, n);
+  const size_t need = workspace_bytes_for(batch, n, single_stream);
   if (workspace_bytes < need || (need > 0 && workspace == nullptr))
     return fail(FASTQR_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
   if (((uintptr_t)workspace & 15) != 0) return fail(FASTQR_EWORKSPACE, "workspace must be 16-byte aligned");
@@ -455,7 +366,7 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   };
   if (use_rowsplit(batch, n)) {
     if ((e = copy_cols(0, ni)) != hipSuccess) return hip_fail(e, "copy launch");
-    return run_rowsplit(H, batch, h_s0, h_s2, tau, tau_s0, tau_s1, Tws, ni, vec, stream);
+    return run_rowsplit(H, batch, h_s0, h_s2, tau, tau_s0, tau_s1, Tws, ni, vec, single_stream, stream);
   }
 
   // Panels are processed in groups of up to 128 columns (kMaxWY transforms
@@ -470,10 +381,11 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
     int g0, pw, g_end, slot_base;
   };
   constexpr int kTw = 32;  // transform width of the strip-resident update
-  std::vector<Group> groups;
-  for (int g0 = 0, gi = 0; g0 < ni; ++gi) {
+  Group groups[kMaxGroups];
+  int ngroups = 0;
+  for (int g0 = 0; g0 < ni; ++ngroups) {
     const int g_end = (g0 + fastqr::kMaxWY * kTw < ni) ? g0 + fastqr::kMaxWY * kTw : ni;
-    groups.push_back(Group{g0, fastqr::panel_width_wide(ni - g0, batch), g_end, (gi % 3) * fastqr::kMaxWY});
+    groups[ngroups] = Group{g0, fastqr::panel_width_wide(ni - g0, batch), g_end, (ngroups % 3) * fastqr::kMaxWY};
     g0 = g_end;
   }
   // narrow updates on the row-split kernels (small batches of tall matrices);
@@ -551,8 +463,11 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   // the narrow update after each panel (one workgroup per matrix and strip)
   // runs beside the wide update too; the wide update has slack (measured on
   // MI355X: 8 x 2048 5% faster; eight CUs per matrix gain nothing more).
+  DeviceAux* aux = (ngroups > 2 && !single_stream) ? device_aux() : nullptr;
   int num_cus = 0, dev = 0;
-  if (hipGetDevice(&dev) != hipSuccess ||
+  if (!aux && ngroups > 2) {
+    num_cus = 0;  // one stream: the wide update has the whole GPU
+  } else if (hipGetDevice(&dev) != hipSuccess ||
       hipDeviceGetAttribute(&num_cus, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
     num_cus = 0;
   int rest_cus = 0;
@@ -568,7 +483,6 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
     });
   };
 
-  DeviceAux* aux = groups.size() > 2 ? device_aux() : nullptr;
   // With the side stream, only the first group's columns are copied before
   // its panels start; the rest of the copy (HBM-bound) runs on the caller's
   // stream beside those panels (latency-bound) and ahead of the first
@@ -576,7 +490,8 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   const int c_first = aux ? groups[0].g_end : ni;
   if ((e = copy_cols(0, c_first)) != hipSuccess) return hip_fail(e, "copy launch");
   if (!aux) {
-    for (const Group& G : groups) {
+    for (int g = 0; g < ngroups; ++g) {
+      const Group& G = groups[g];
       e = run_panels(G, stream);
       if (e == hipSuccess) e = run_update(G, G.g_end, ni, false, stream);
       if (e != hipSuccess) return hip_fail(e, "blocked launch");
@@ -605,8 +520,8 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   // columns of the next look-ahead update ready (first: the copy)
   hipEvent_t ev_near = c_first < ni ? record(stream) : nullptr;
   if (c_first < ni && !ev_near) return fail(FASTQR_EINVAL, "cannot record HIP events");
-  std::vector<hipEvent_t> ev_rest(groups.size(), nullptr);  // group g's wide update ended
-  for (size_t g = 0; g + 1 < groups.size(); ++g) {
+  hipEvent_t ev_rest[kMaxGroups] = {};  // group g's wide update ended
+  for (int g = 0; g + 1 < ngroups; ++g) {
     const Group& G = groups[g];
     const Group& Nx = groups[g + 1];
     if (ev_near && (e = hipStreamWaitEvent(side, ev_near, 0)) != hipSuccess) return hip_fail(e, "stream join");
@@ -617,7 +532,7 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
     if ((e = run_panels(Nx, side)) != hipSuccess) return hip_fail(e, "panel launch");
     if ((e = hipStreamWaitEvent(stream, ev_la, 0)) != hipSuccess) return hip_fail(e, "stream join");
     ev_near = nullptr;
-    if (g + 2 < groups.size()) {
+    if (g + 2 < ngroups) {
       const Group& N2 = groups[g + 2];
       if ((e = run_update(G, N2.g0, N2.g_end, false, stream)) != hipSuccess) return hip_fail(e, "update launch");
       if (!(ev_near = record(stream))) return fail(FASTQR_EINVAL, "cannot record HIP events");
@@ -629,6 +544,175 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int
   if (!ev_end) return fail(FASTQR_EINVAL, "cannot record HIP events");
   if ((e = hipStreamWaitEvent(stream, ev_end, 0)) != hipSuccess) return hip_fail(e, "stream join");
   return FASTQR_OK;
+}
+
+// ---- fastqr_geqrf_f32_noalloc: scratch in a static device array ------------
+// The blocked path's T factors (and the row-split partial products) live in
+// `scratch`, one copy per GPU, held until the process ends.  Its device address
+// is taken once per device with hipGetSymbolAddress (the array's name is only a
+// host-side stand-in) and kept in g_scratch_ptr; kernels only ever see that
+// address.  Every call on a GPU shares the array: calls that overlap in time on
+// one GPU (two streams, two threads) race on it.  Nothing in it has to start at
+// zero: every T slot and partial product is written before it is read.
+__device__ __align__(256) unsigned char scratch[FASTQR_NOALLOC_SCRATCH_BYTES];
+
+constexpr int kMaxDevices = 64;
+std::atomic<void*> g_scratch_ptr[kMaxDevices];
+
+// Device address of the current device's `scratch`.
+int noalloc_scratch(void** out) {
+  int dev = -1;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_fail(e, "hipGetDevice");
+  if (dev < 0 || dev >= kMaxDevices) return fail(FASTQR_EINVAL, "device %d beyond the %d supported", dev, kMaxDevices);
+  void* p = g_scratch_ptr[dev].load(std::memory_order_acquire);
+  if (p == nullptr) {
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_fail(e, "hipGetSymbolAddress(scratch)");
+    if (p == nullptr) return fail(FASTQR_EWORKSPACE, "hipGetSymbolAddress(scratch) returned NULL");
+    g_scratch_ptr[dev].store(p, std::memory_order_release);
+  }
+  *out = p;
+  return FASTQR_OK;
+}
+
+}  // namespace
+
+extern "C" {
+
+int fastqr_profile_enable(int on) {
+  if (on) {
+    (void)g_prof.drain();
+    for (Totals& t : g_prof.totals) t = Totals{};
+  }
+  g_prof.on = on != 0;
+  return FASTQR_OK;
+}
+
+int fastqr_profile_collect(int kind, int64_t* launches, double* milliseconds, double* flops, double* bytes) {
+  if (kind < 0 || kind >= FASTQR_PROFILE_KINDS) return fail(FASTQR_EINVAL, "profile kind %d out of range", kind);
+  const hipError_t e = g_prof.drain();
+  const Totals& t = g_prof.totals[kind];
+  if (launches) *launches = t.launches;
+  if (milliseconds) *milliseconds = t.ms;
+  if (flops) *flops = t.flops;
+  if (bytes) *bytes = t.bytes;
+  return e == hipSuccess ? FASTQR_OK : hip_fail(e, "profile collect");
+}
+
+const char* fastqr_profile_kind_name(int kind) {
+  return (kind >= 0 && kind < FASTQR_PROFILE_KINDS) ? kKindNames[kind] : "";
+}
+
+int fastqr_version(void) { return 1; }
+
+const char* fastqr_last_error(void) { return g_last_error; }
+
+void fastqr_debug_force_error(int code) { g_forced_error = code; }
+
+const char* fastqr_path_name(int64_t n) {
+  if (n <= kWaveMaxN) return "wave64";
+  if (n <= fastqr::kLdsMaxN) return "lds";
+  return "blocked";
+}
+
+size_t fastqr_workspace_bytes(int64_t batch, int64_t n) { return workspace_bytes_for(batch, n, false); }
+
+size_t fastqr_orgqr_workspace_bytes(int64_t batch, int64_t n) {
+  if (batch <= 0 || n <= 0 || n > kMaxN) return 0;
+  // the batch is processed in chunks of at most kMaxGridY matrices
+  const int64_t chunk = batch < fastqr::kMaxGridY ? batch : fastqr::kMaxGridY;
+  return (fastqr::orgqr_workspace_floats(chunk, (int)n) * sizeof(float) + 255) & ~(size_t)255;
+}
+
+int fastqr_orgqr_f32(const float* H, int64_t batch, int64_t n, int64_t h_s0, int64_t h_s1, int64_t h_s2,
+                     const float* tau, int64_t tau_s0, int64_t tau_s1, float* Q, int64_t q_s0, int64_t q_s1,
+                     int64_t q_s2, void* workspace, size_t workspace_bytes, void* stream_ptr) {
+  g_last_error[0] = '\0';
+  if (g_forced_error != 0) {
+    const int code = g_forced_error;
+    g_forced_error = 0;
+    return fail(code, "forced error %d (test hook)", code);
+  }
+  if (batch < 0 || n < 0) return fail(FASTQR_EINVAL, "batch and n must be non-negative (got %lld, %lld)",
+                                      (long long)batch, (long long)n);
+  if (batch == 0 || n == 0) return FASTQR_OK;
+  if (n > kMaxN) return fail(FASTQR_EINVAL, "n=%lld exceeds the supported maximum %lld", (long long)n,
+                             (long long)kMaxN);
+  if (batch > 2147483647LL) return fail(FASTQR_EINVAL, "batch too large");
+  if (!H || !tau || !Q) return fail(FASTQR_EINVAL, "H, tau and Q must be non-null device pointers");
+  if (h_s0 < 0 || h_s1 < 0 || h_s2 < 0 || q_s0 < 0 || q_s2 < 0 || tau_s0 < 0 || tau_s1 < 0)
+    return fail(FASTQR_EINVAL, "negative strides are not supported");
+  if (batch > 1 && (q_s0 == 0 || tau_s0 == 0))
+    return fail(FASTQR_EINVAL, "Q and tau batch strides must be non-zero when batch > 1");
+  if (n > 1 && (tau_s1 == 0 || h_s1 == 0 || h_s2 == 0)) return fail(FASTQR_EINVAL, "H and tau strides must be non-zero");
+  if (q_s1 != 1 || q_s2 < n)
+    return fail(FASTQR_ELAYOUT, "Q must have contiguous columns (stride (*, 1, >=n)); got (%lld, %lld, %lld)",
+                (long long)q_s0, (long long)q_s1, (long long)q_s2);
+  if (q_s2 * n * 4 >= (int64_t)1 << 31)
+    return fail(FASTQR_ELAYOUT, "one matrix of Q spans %lld bytes; at most 2 GiB are addressed",
+                (long long)(q_s2 * n * 4));
+  if (batch > 1 && q_s0 < q_s2 * n)
+    return fail(FASTQR_ELAYOUT, "Q batch stride %lld smaller than one matrix (%lld)", (long long)q_s0,
+                (long long)(q_s2 * n));
+  const size_t need = fastqr_orgqr_workspace_bytes(batch, n);
+  if (workspace_bytes < need || (need > 0 && workspace == nullptr))
+    return fail(FASTQR_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+  if (((uintptr_t)workspace & 15) != 0) return fail(FASTQR_EWORKSPACE, "workspace must be 16-byte aligned");
+  const bool same = ((const float*)Q == H && q_s0 == h_s0 && q_s1 == h_s1 && q_s2 == h_s2);
+  const int64_t q_span = span_elems(batch, n, q_s0, 1, q_s2);
+  if (!same && ranges_overlap(H, span_elems(batch, n, h_s0, h_s1, h_s2), Q, q_span))
+    return fail(FASTQR_EOVERLAP, "H and Q overlap with different layouts");
+  if (ranges_overlap(tau, span_elems(batch, n, tau_s0, tau_s1, 0), Q, q_span))
+    return fail(FASTQR_EOVERLAP, "tau and Q overlap");
+  const bool vec = ((uintptr_t)Q % 16 == 0) && (q_s0 % 4 == 0) && (q_s2 % 4 == 0) && (n % 4 == 0);
+  // chunks of at most kMaxGridY matrices (its kernels put the batch in grid.y),
+  // one after another on the stream, sharing the workspace
+  for (int64_t b0 = 0; b0 < batch; b0 += fastqr::kMaxGridY) {
+    const int64_t nb = (batch - b0 < fastqr::kMaxGridY) ? batch - b0 : fastqr::kMaxGridY;
+    const hipError_t e = fastqr::launch_orgqr(H + b0 * h_s0, nb, (int)n, h_s0, h_s1, h_s2, tau + b0 * tau_s0, tau_s0,
+                                              tau_s1, Q + b0 * q_s0, q_s0, q_s2, (float*)workspace, vec,
+                                              (hipStream_t)stream_ptr);
+    if (e != hipSuccess) return hip_fail(e, "orgqr launch");
+  }
+  return FASTQR_OK;
+}
+
+int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a_s1, int64_t a_s2,
+                     float* H, int64_t h_s0, int64_t h_s1, int64_t h_s2, float* tau, int64_t tau_s0,
+                     int64_t tau_s1, void* workspace, size_t workspace_bytes, void* stream_ptr) {
+  g_last_error[0] = '\0';
+  if (g_forced_error != 0) {
+    const int code = g_forced_error;
+    g_forced_error = 0;
+    return fail(code, "forced error %d (test hook)", code);
+  }
+  return geqrf_impl(A, batch, n, a_s0, a_s1, a_s2, H, h_s0, h_s1, h_s2, tau, tau_s0, tau_s1, workspace,
+                    workspace_bytes, false, stream_ptr);
+}
+
+int fastqr_geqrf_f32_noalloc(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a_s1, int64_t a_s2,
+                             float* H, int64_t h_s0, int64_t h_s1, int64_t h_s2, float* tau, int64_t tau_s0,
+                             int64_t tau_s1, void* stream_ptr) {
+  g_last_error[0] = '\0';
+  if (g_forced_error != 0) {
+    const int code = g_forced_error;
+    g_forced_error = 0;
+    return fail(code, "forced error %d (test hook)", code);
+  }
+  const size_t need = workspace_bytes_for(batch, n, true);
+  if (need > (size_t)FASTQR_NOALLOC_SCRATCH_BYTES)
+    return fail(FASTQR_EWORKSPACE,
+                "batch=%lld n=%lld needs %zu bytes of scratch; fastqr_geqrf_f32_noalloc holds at most %zu "
+                "(split the batch, or call fastqr_geqrf_f32 with a workspace)",
+                (long long)batch, (long long)n, need, (size_t)FASTQR_NOALLOC_SCRATCH_BYTES);
+  void* ws = nullptr;
+  if (need > 0) {
+    const int rc = noalloc_scratch(&ws);
+    if (rc != FASTQR_OK) return rc;
+  }
+  return geqrf_impl(A, batch, n, a_s0, a_s1, a_s2, H, h_s0, h_s1, h_s2, tau, tau_s0, tau_s1, ws,
+                    need > 0 ? (size_t)FASTQR_NOALLOC_SCRATCH_BYTES : 0, true, stream_ptr);
 }
 
 }  // extern "C"

@@ -22,10 +22,13 @@ FASTQR_EWORKSPACE = -2
 FASTQR_ELAYOUT = -3
 FASTQR_EOVERLAP = -4
 FASTQR_ETESTHOOK = -99
+# size of the static device scratch of fastqr_geqrf_f32_noalloc (FASTQR_NOALLOC_SCRATCH_BYTES)
+NOALLOC_SCRATCH_BYTES = 32 << 20
 
 # every symbol include/fastqr.h declares
 EXPORTED_SYMBOLS = (
     "fastqr_geqrf_f32",
+    "fastqr_geqrf_f32_noalloc",
     "fastqr_workspace_bytes",
     "fastqr_orgqr_f32",
     "fastqr_orgqr_workspace_bytes",
@@ -72,6 +75,8 @@ def cdll() -> ctypes.CDLL:
         i64, vp, sz = ctypes.c_int64, ctypes.c_void_p, ctypes.c_size_t
         lib.fastqr_geqrf_f32.argtypes = [vp, i64, i64, i64, i64, i64, vp, i64, i64, i64, vp, i64, i64, vp, sz, vp]
         lib.fastqr_geqrf_f32.restype = ctypes.c_int
+        lib.fastqr_geqrf_f32_noalloc.argtypes = [vp, i64, i64, i64, i64, i64, vp, i64, i64, i64, vp, i64, i64, vp]
+        lib.fastqr_geqrf_f32_noalloc.restype = ctypes.c_int
         lib.fastqr_workspace_bytes.argtypes = [i64, i64]
         lib.fastqr_orgqr_f32.argtypes = [vp, i64, i64, i64, i64, i64, vp, i64, i64, vp, i64, i64, i64, vp, sz, vp]
         lib.fastqr_orgqr_f32.restype = ctypes.c_int

@@ -80,6 +80,31 @@ int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n,
 size_t fastqr_workspace_bytes(int64_t batch, int64_t n);
 
 /*
+ * fastqr_geqrf_f32 without a workspace argument, for callers that cannot
+ * allocate device memory (code under HIP graph capture, serving loops and
+ * harnesses that forbid hipMalloc).  No counterpart in the reference.
+ *
+ * Same arguments, results and errors as fastqr_geqrf_f32 minus the workspace:
+ * the scratch it needs (fastqr_workspace_bytes(batch, n) bytes, less for
+ * n > 2048, where one stream needs one set of partial products instead of
+ * two) is a static device array of FASTQR_NOALLOC_SCRATCH_BYTES inside the
+ * library, one per GPU, held until the process ends.  Calls needing more
+ * return FASTQR_EWORKSPACE without launching anything (split the batch, or
+ * use fastqr_geqrf_f32): up to 682 matrices for 176 < n <= 1024, one matrix
+ * for 2048 < n <= 2100; none above.  It calls no hipMalloc/hipFree and creates no stream or
+ * event: every kernel runs on `stream`, in order (the blocked path's panel
+ * look-ahead on a second stream is not used).  All calls on one GPU share the
+ * array, so calls that overlap in time on one GPU (different streams or
+ * threads) race and must be serialised by the caller.
+ */
+#define FASTQR_NOALLOC_SCRATCH_BYTES ((size_t)32 << 20)
+int fastqr_geqrf_f32_noalloc(const float* A, int64_t batch, int64_t n,
+                             int64_t a_s0, int64_t a_s1, int64_t a_s2,
+                             float* H, int64_t h_s0, int64_t h_s1, int64_t h_s2,
+                             float* tau, int64_t tau_s0, int64_t tau_s1,
+                             void* stream);
+
+/*
  * Explicit Q of batched compact-Householder factors: Q = H_0 H_1 ... H_{n-1}
  * with H_k = I - tau[k] v_k v_k^T, v_k below the diagonal of column k of H
  * (implicit unit at row k).  Replaces torch.linalg.householder_product(H, tau),

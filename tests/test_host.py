@@ -93,6 +93,24 @@ def test_argument_validation_returns_codes_without_launching():
     assert _call(lib, a_s=(-1, 100, 1)) == _lib.FASTQR_EINVAL
 
 
+def test_noalloc_rejects_sizes_beyond_its_scratch_without_launching():
+    # fake, never-dereferenced addresses: the size check comes before any HIP call
+    lib = fastqr.cdll()
+    base = 1 << 40
+
+    def call(b, n):
+        return lib.fastqr_geqrf_f32_noalloc(8 * base, b, n, n * n, n, 1, 16 * base, n * n, 1, n, 32 * base, n, 1,
+                                            None)
+
+    assert lib.fastqr_workspace_bytes(683, 512) > _lib.NOALLOC_SCRATCH_BYTES >= lib.fastqr_workspace_bytes(682, 512)
+    assert call(683, 512) == _lib.FASTQR_EWORKSPACE
+    assert b"fastqr_geqrf_f32_noalloc holds at most" in lib.fastqr_last_error()
+    assert call(2, 4096) == _lib.FASTQR_EWORKSPACE
+    assert call(2, 2100) == _lib.FASTQR_EWORKSPACE
+    assert call(0, 512) == _lib.FASTQR_OK  # empty batch: nothing to do
+    assert call(1, 9000) == _lib.FASTQR_EINVAL
+
+
 def test_forced_error_hook_round_trip():
     lib = fastqr.cdll()
     lib.fastqr_debug_force_error(-99)
