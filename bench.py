@@ -83,6 +83,9 @@ def parse_args():
     p.add_argument("--eval-cases", metavar="I,J,...", help="with --eval-contract: only these benchmark cases (0-based)")
     p.add_argument("--eval-max-time-ns", type=float, default=10e9,
                    help="with --eval-contract: per-case kernel-time budget of the stopping rule (evaluator: 10 s)")
+    p.add_argument("--summarize-counters", metavar="PMC_DIR",
+                   help="print per-kernel MFMA / VALU utilisation from a rocprofv3 --pmc run of this script with "
+                        + " ".join(UTIL_COUNTERS) + ", and exit")
     p.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                    help="print per-kernel statistics of a rocprofv3 --kernel-trace run of this script, split into "
                         "the geqrf calls and the householder_product calls, and exit")
@@ -184,6 +187,87 @@ def summarize_traffic(fetch_dir: str, write_dir: str) -> str:
         fb = ent["FETCH_SIZE"][1] / n
         wb = ent["WRITE_SIZE"][1] / max(ent["WRITE_SIZE"][0], 1)
         lines.append(f"| {kind} | {n} | {fb / 2**20:.2f} | {wb / 2**20:.2f} | {fb + wb:.6g} |")
+    lines.append("")
+    return "\n".join(lines)
+
+
+# MFMA / VALU utilisation counters (one rocprofv3 --pmc pass: 6 SQ + 1 GRBM)
+UTIL_COUNTERS = ("SQ_INSTS_VALU_MFMA_MOPS_F32", "SQ_VALU_MFMA_BUSY_CYCLES", "SQ_ACTIVE_INST_VALU", "SQ_INSTS_VALU",
+                 "SQ_INSTS_MFMA", "SQ_BUSY_CYCLES", "GRBM_GUI_ACTIVE")
+MI355X_CUS, MI355X_SIMDS = 256, 1024
+
+
+def summarize_counters(directory: str) -> str:
+    """Markdown: per kernel kind, MFMA and VALU utilisation from a rocprofv3
+    --pmc pass, each dispatch normalised by its own duration (End - Start of
+    the dispatch at the nominal 2.4 GHz; GRBM_GUI_ACTIVE also spans the
+    profiler's sampling window, ~120 us more than a 10 us kernel):
+      MfmaUtil  = sum SQ_VALU_MFMA_BUSY_CYCLES / (cycles x 1024 SIMDs),
+      VALUBusy  = sum SQ_ACTIVE_INST_VALU / 256 CUs / cycles (rocprofv3's
+                  formula with the dispatch's cycles), and the same over the
+                  CUs the launch can occupy (min(workgroups, 256)),
+      MFMA fp32 TFLOP/s = SQ_INSTS_VALU_MFMA_MOPS_F32 x 512 / duration."""
+    import csv
+    import glob
+
+    paths = glob.glob(os.path.join(directory, "**", "*counter_collection.csv"), recursive=True)
+    if not paths:
+        raise SystemExit(f"no counter_collection.csv under {directory}")
+    per = {}
+    for row in csv.DictReader(open(paths[0])):
+        d = per.setdefault(row["Dispatch_Id"], {
+            "name": row["Kernel_Name"],
+            "ns": int(row["End_Timestamp"]) - int(row["Start_Timestamp"]),
+            "wgs": max(1, int(row["Grid_Size"]) // max(1, int(row["Workgroup_Size"]))),
+            "vals": {}})
+        d["vals"][row["Counter_Name"]] = d["vals"].get(row["Counter_Name"], 0.0) + float(row["Counter_Value"])
+    agg = {}
+    for d in per.values():
+        kind = next((k for key, k in KIND_OF if key in d["name"]), None)
+        if kind is None or "fastqr" not in d["name"]:
+            continue
+        v = d["vals"]
+        cyc = d["ns"] * 2.4
+        a = agg.setdefault(kind, {"launches": 0, "ns": 0.0, "mfma_busy": 0.0, "valu_active": 0.0, "valu_cu_cyc": 0.0,
+                                  "mops": 0.0, "insts_valu": 0.0, "insts_mfma": 0.0})
+        a["launches"] += 1
+        a["ns"] += d["ns"]
+        a["mfma_busy"] += v.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0)
+        a["valu_active"] += v.get("SQ_ACTIVE_INST_VALU", 0.0)
+        a["valu_cu_cyc"] += min(d["wgs"], MI355X_CUS) * cyc
+        a["mops"] += v.get("SQ_INSTS_VALU_MFMA_MOPS_F32", 0.0)
+        a["insts_valu"] += v.get("SQ_INSTS_VALU", 0.0)
+        a["insts_mfma"] += v.get("SQ_INSTS_MFMA", 0.0)
+    lines = [
+        "# MFMA and VALU utilisation per kernel kind — bench.py, all five workloads (one step, geqrf calls only)",
+        "",
+        "Command (repository root on one MI355X; `$REPO` the repository root, `$OUT` an output directory):",
+        "",
+        "```",
+        "cd /tmp && rocprofv3 --pmc " + " ".join(UTIL_COUNTERS) + " -d $OUT/pmc_util -o run -f csv -- python3 "
+        "$REPO/bench.py --steps 1 --warmup 0 --no-profile --no-check --cpu-sample-seconds 0 --no-orgqr --no-colmajor",
+        "python3 bench.py --summarize-counters $OUT/pmc_util > profiles/mfma_valu_utilisation_bench_all_workloads.md",
+        "```",
+        "",
+        "Counter collection serialises the launches, so each kernel runs alone on the GPU here. Every dispatch is "
+        "normalised by its own duration at the nominal 2.4 GHz (GRBM_GUI_ACTIVE also spans the profiler's sampling "
+        "window). MfmaUtil = sum SQ_VALU_MFMA_BUSY_CYCLES / (cycles x %d SIMDs); VALUBusy = sum "
+        "SQ_ACTIVE_INST_VALU / %d CUs / cycles (rocprofv3's derived formula), and per occupied CU = the same over "
+        "min(workgroups, 256) CUs; MFMA TFLOP/s = SQ_INSTS_VALU_MFMA_MOPS_F32 x 512 / duration (peak 157.3)."
+        % (MI355X_SIMDS, MI355X_CUS),
+        "",
+        "| kernel kind | launches | kernel ms | MfmaUtil % | MFMA fp32 TFLOP/s counted | VALUBusy % | "
+        "VALUBusy % per occupied CU | VALU insts | MFMA insts |",
+        "|---|---:|---:|---:|---:|---:|---:|---:|---:|",
+    ]
+    for kind, a in sorted(agg.items()):
+        cyc = max(a["ns"] * 2.4, 1.0)
+        mfma_util = 100.0 * a["mfma_busy"] / (cyc * MI355X_SIMDS)
+        valu_busy = 100.0 * a["valu_active"] / MI355X_CUS / cyc
+        valu_occ = 100.0 * a["valu_active"] / max(a["valu_cu_cyc"], 1.0)
+        tflops = a["mops"] * 512 / max(a["ns"] * 1e-9, 1e-12) / 1e12
+        lines.append(f"| {kind} | {a['launches']} | {a['ns'] / 1e6:.3f} | {mfma_util:.1f} | {tflops:.1f} | "
+                     f"{valu_busy:.1f} | {valu_occ:.1f} | {a['insts_valu']:.4g} | {a['insts_mfma']:.4g} |")
     lines.append("")
     return "\n".join(lines)
 
@@ -338,6 +422,9 @@ def main() -> int:
     args = parse_args()
     if args.summarize_traffic:
         print(summarize_traffic(*args.summarize_traffic))
+        return 0
+    if args.summarize_counters:
+        print(summarize_counters(args.summarize_counters))
         return 0
     if args.summarize_trace:
         print(summarize_trace(args.summarize_trace))

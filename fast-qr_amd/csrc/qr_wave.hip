@@ -192,7 +192,9 @@ struct WaveQR {
   }
 };
 
-template <int NT>
+// CM: A is column-major with 16-byte aligned columns (chosen on the host, so
+// the row-major kernel carries no extra branch).
+template <int NT, bool CM>
 __global__ void __launch_bounds__(64) qr_wave_kernel(const float* __restrict__ A, int64_t as0, int64_t as1,
                                                       int64_t as2, float* __restrict__ H, int64_t hs0, int64_t hs1,
                                                       int64_t hs2, float* __restrict__ tau, int64_t ts0, int64_t ts1,
@@ -203,17 +205,16 @@ __global__ void __launch_bounds__(64) qr_wave_kernel(const float* __restrict__ A
   q.kq = lane >> 4;
   q.cn = lane & 15;
   const float* Ab = A + b * as0;
-  // Column-major source with 16-byte aligned columns: a lane's four rows of a
-  // column are one 16-byte load (four lanes cover 64 contiguous bytes of each
-  // column).  Otherwise one element per load, lanes along the columns of a row.
-  const bool a_vec = as1 == 1 && (as2 & 3) == 0 && (as0 & 3) == 0 && ((uintptr_t)A & 15) == 0;
+  // Column-major source (CM): a lane's four rows of a column are one 16-byte
+  // load (four lanes cover 64 contiguous bytes of each column).  Otherwise one
+  // element per load, lanes along the columns of a row.
 #pragma unroll
   for (int tr = 0; tr < NT; ++tr) {
 #pragma unroll
     for (int tc = 0; tc < NT; ++tc) {
       const int c = 16 * tc + q.cn;
       const int r0 = 16 * tr + 4 * q.kq;
-      if (a_vec && c < n && r0 + 3 < n) {
+      if (CM && c < n && r0 + 3 < n) {
         q.X[tr][tc] = *reinterpret_cast<const f32x4*>(Ab + c * as2 + r0);
       } else {
 #pragma unroll
@@ -258,8 +259,14 @@ hipError_t launch_qr_wave(const float* A, int64_t batch, int n, int64_t as0, int
                           hipStream_t stream) {
   const dim3 grid((unsigned)batch);
   const dim3 block(64);
-#define FASTQR_WAVE_LAUNCH(NT) \
-  hipLaunchKernelGGL((qr_wave_kernel<NT>), grid, block, 0, stream, A, as0, as1, as2, H, hs0, hs1, hs2, tau, ts0, ts1, n)
+  const bool cm = as1 == 1 && (as2 & 3) == 0 && (as0 & 3) == 0 && ((uintptr_t)A & 15) == 0;
+#define FASTQR_WAVE_LAUNCH(NT)                                                                                  \
+  if (cm)                                                                                                       \
+    hipLaunchKernelGGL((qr_wave_kernel<NT, true>), grid, block, 0, stream, A, as0, as1, as2, H, hs0, hs1, hs2, \
+                       tau, ts0, ts1, n);                                                                       \
+  else                                                                                                          \
+    hipLaunchKernelGGL((qr_wave_kernel<NT, false>), grid, block, 0, stream, A, as0, as1, as2, H, hs0, hs1, hs2, \
+                       tau, ts0, ts1, n)
   if (n <= 16) {
     FASTQR_WAVE_LAUNCH(1);
   } else if (n <= 32) {
