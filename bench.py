@@ -64,7 +64,8 @@ def parse_args():
     p.add_argument("--no-check", action="store_true", help="skip the post-timing recheck")
     p.add_argument("--no-profile", action="store_true", help="skip the instrumented per-kernel pass")
     p.add_argument("--no-orgqr", action="store_true",
-                   help="skip timing householder_product (explicit Q from the factors) per shape")
+                   help="skip timing householder_product (explicit Q from the factors) and apply_q (Q^T A "
+                        "without forming Q) per shape")
     p.add_argument("--official", action="store_true",
                    help="time the task's own 12 benchmark cases (official/task.yml) instead of the five workloads; "
                         "value = geomean over the 12 cases")
@@ -582,6 +583,7 @@ def main() -> int:
     # ---- explicit Q: householder_product on each timed input's factors --------------
     # (the reference checker's consumer of (H, tau), official/reference.py:199)
     orgqr_us = {}
+    ormqr_us = {}
     if not args.no_orgqr:
         for _, s in shapes:
             facs = run_shape(s.label)
@@ -599,6 +601,22 @@ def main() -> int:
                 torch.cuda.synchronize()
                 times.append(e0.elapsed_time(e1) * 1e3 / len(facs))
             orgqr_us[s.label] = statistics.median(times)
+            # Q^T A without forming Q (torch.ormqr's meaning): C = the input itself
+            a_in = data[s.label]
+            fastqr.apply_q(*facs[0], a_in[0], transpose=True)  # warm
+            torch.cuda.synchronize()
+            times = []
+            for _ in range(max(1, args.steps)):
+                flush_buf.fill_(42)
+                e0 = torch.cuda.Event(enable_timing=True)
+                e1 = torch.cuda.Event(enable_timing=True)
+                e0.record()
+                for (h, tau), a in zip(facs, a_in):
+                    fastqr.apply_q(h, tau, a, transpose=True)
+                e1.record()
+                torch.cuda.synchronize()
+                times.append(e0.elapsed_time(e1) * 1e3 / len(facs))
+            ormqr_us[s.label] = statistics.median(times)
             del facs
 
     # ---- CPU baseline: torch.geqrf on this host's cores ------------------------
@@ -628,6 +646,10 @@ def main() -> int:
                 t = time.perf_counter_ns()
                 torch.linalg.householder_product(h_c, t_c)
                 cpu[s.label]["orgqr_us"] = (time.perf_counter_ns() - t) / 1e3 * s.batch / k
+                torch.ormqr(h_c, t_c, sample, left=True, transpose=True)  # warm
+                t = time.perf_counter_ns()
+                torch.ormqr(h_c, t_c, sample, left=True, transpose=True)
+                cpu[s.label]["ormqr_us"] = (time.perf_counter_ns() - t) / 1e3 * s.batch / k
 
     # ---- report ---------------------------------------------------------------------
     shape_rows = {}
@@ -683,6 +705,19 @@ def main() -> int:
                     row["householder_product"]["cpu_us"] = round(cpu[s.label]["orgqr_us"], 1)
                 log(f"[gpu] {s.label}: householder_product {qu:9.1f} us/call "
                     f"{row['householder_product']['gflops']:9.1f} GFLOP/s")
+            if s.label in ormqr_us:
+                au = ormqr_us[s.label]
+                afl = s.batch * 2.0 * s.n ** 3  # sormqr, m = k = r = n: 2 k r (2m - r)
+                row["apply_q"] = {
+                    "op": "Q^T A (torch.ormqr transpose=True, C = A)",
+                    "us_per_call": round(au, 3),
+                    "gflops": round(afl / (au * 1e-6) / 1e9, 2),
+                    "pct_fp32_peak": round(100.0 * afl / (au * 1e-6) / (PEAK_FP32_TFLOPS * 1e12), 2),
+                }
+                if "ormqr_us" in cpu.get(s.label, {}):
+                    row["apply_q"]["cpu_us"] = round(cpu[s.label]["ormqr_us"], 1)
+                log(f"[gpu] {s.label}: apply_q (Q^T A)   {au:9.1f} us/call "
+                    f"{row['apply_q']['gflops']:9.1f} GFLOP/s")
             if s.label in cpu:
                 row["cpu_geqrf_us"] = round(cpu[s.label]["us_per_call"], 1)
                 row["speedup_vs_cpu"] = round(cpu[s.label]["us_per_call"] / us, 1)
@@ -766,6 +801,7 @@ def main() -> int:
             "geomean_shapes_us": round(geomean([r["us_per_call"] for r in shape_rows.values()]), 3),
             "householder_product_geomean_shapes_us": (round(geomean(list(orgqr_us.values())), 3)
                                                       if orgqr_us else None),
+            "apply_q_geomean_shapes_us": round(geomean(list(ormqr_us.values())), 3) if ormqr_us else None,
             "shapes": shape_rows,
             "c2_column_major": colmajor or None,
         },

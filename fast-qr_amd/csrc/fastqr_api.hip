@@ -678,6 +678,70 @@ int fastqr_orgqr_f32(const float* H, int64_t batch, int64_t n, int64_t h_s0, int
   return FASTQR_OK;
 }
 
+size_t fastqr_ormqr_workspace_bytes(int64_t batch, int64_t r) {
+  if (batch <= 0 || r <= 0 || r > kMaxN) return 0;
+  const int64_t chunk = batch < fastqr::kMaxGridY ? batch : fastqr::kMaxGridY;
+  return (fastqr::ormqr_workspace_floats(chunk, (int)r) * sizeof(float) + 255) & ~(size_t)255;
+}
+
+int fastqr_ormqr_f32(const float* H, int64_t batch, int64_t m, int64_t r, int64_t h_s0, int64_t h_s1, int64_t h_s2,
+                     const float* tau, int64_t tau_s0, int64_t tau_s1, float* C, int64_t k, int64_t c_s0,
+                     int64_t c_s1, int64_t c_s2, int transpose, void* workspace, size_t workspace_bytes,
+                     void* stream_ptr) {
+  g_last_error[0] = '\0';
+  if (g_forced_error != 0) {
+    const int code = g_forced_error;
+    g_forced_error = 0;
+    return fail(code, "forced error %d (test hook)", code);
+  }
+  if (batch < 0 || m < 0 || r < 0 || k < 0)
+    return fail(FASTQR_EINVAL, "batch, m, r and k must be non-negative (got %lld, %lld, %lld, %lld)",
+                (long long)batch, (long long)m, (long long)r, (long long)k);
+  if (r > m) return fail(FASTQR_EINVAL, "r=%lld reflectors exceed m=%lld rows", (long long)r, (long long)m);
+  if (batch == 0 || m == 0 || k == 0 || r == 0) return FASTQR_OK;  // nothing to apply (Q = I when r == 0)
+  if (m > kMaxN) return fail(FASTQR_EINVAL, "m=%lld exceeds the supported maximum %lld", (long long)m,
+                             (long long)kMaxN);
+  if (batch > 2147483647LL || k > 2147483647LL) return fail(FASTQR_EINVAL, "batch or k too large");
+  if (!H || !tau || !C) return fail(FASTQR_EINVAL, "H, tau and C must be non-null device pointers");
+  if (h_s0 < 0 || h_s2 < 0 || c_s0 < 0 || c_s2 < 0 || tau_s0 < 0 || tau_s1 < 0)
+    return fail(FASTQR_EINVAL, "negative strides are not supported");
+  if (batch > 1 && c_s0 == 0) return fail(FASTQR_EINVAL, "C batch stride must be non-zero when batch > 1");
+  if (r > 1 && tau_s1 == 0) return fail(FASTQR_EINVAL, "tau column stride must be non-zero");
+  if (h_s1 != 1 || h_s2 < m)
+    return fail(FASTQR_ELAYOUT, "H must have contiguous columns (stride (*, 1, >=m)); got (%lld, %lld, %lld)",
+                (long long)h_s0, (long long)h_s1, (long long)h_s2);
+  if (c_s1 != 1 || c_s2 < m)
+    return fail(FASTQR_ELAYOUT, "C must have contiguous columns (stride (*, 1, >=m)); got (%lld, %lld, %lld)",
+                (long long)c_s0, (long long)c_s1, (long long)c_s2);
+  // 32-bit byte offsets up to the end of the last (partial) 32-column block
+  if (h_s2 * ((r + 31) & ~31LL) * 4 >= (int64_t)1 << 31 || c_s2 * ((k + 31) & ~31LL) * 4 >= (int64_t)1 << 31)
+    return fail(FASTQR_ELAYOUT, "one matrix of H or C spans more than the 2 GiB a launch addresses");
+  if (batch > 1 && c_s0 < c_s2 * k)
+    return fail(FASTQR_ELAYOUT, "C batch stride %lld smaller than one matrix (%lld)", (long long)c_s0,
+                (long long)(c_s2 * k));
+  const size_t need = fastqr_ormqr_workspace_bytes(batch, r);
+  if (workspace_bytes < need || (need > 0 && workspace == nullptr))
+    return fail(FASTQR_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
+  if (((uintptr_t)workspace & 15) != 0) return fail(FASTQR_EWORKSPACE, "workspace must be 16-byte aligned");
+  const int64_t c_span = span_elems(batch, m, c_s0, 1, 0) + (k - 1) * c_s2;
+  if (ranges_overlap(H, span_elems(batch, m, h_s0, 1, 0) + (r - 1) * h_s2, C, c_span))
+    return fail(FASTQR_EOVERLAP, "H and C overlap");
+  if (ranges_overlap(tau, span_elems(batch, r, tau_s0, tau_s1, 0), C, c_span))
+    return fail(FASTQR_EOVERLAP, "tau and C overlap");
+  // 16-byte column segments when every column of H and C starts 16-byte aligned and m rows fill them
+  const bool vec = ((uintptr_t)H % 16 == 0) && (h_s0 % 4 == 0) && (h_s2 % 4 == 0) && ((uintptr_t)C % 16 == 0) &&
+                   (c_s0 % 4 == 0) && (c_s2 % 4 == 0) && (m % 4 == 0);
+  // chunks of at most kMaxGridY matrices (the T kernel puts the batch in grid.y)
+  for (int64_t b0 = 0; b0 < batch; b0 += fastqr::kMaxGridY) {
+    const int64_t nb = (batch - b0 < fastqr::kMaxGridY) ? batch - b0 : fastqr::kMaxGridY;
+    const hipError_t e = fastqr::launch_ormqr(H + b0 * h_s0, nb, (int)m, (int)r, h_s0, h_s2, tau + b0 * tau_s0, tau_s0,
+                                              tau_s1, C + b0 * c_s0, c_s0, c_s2, (int)k, transpose != 0,
+                                              (float*)workspace, vec, (hipStream_t)stream_ptr);
+    if (e != hipSuccess) return hip_fail(e, "ormqr launch");
+  }
+  return FASTQR_OK;
+}
+
 int fastqr_geqrf_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a_s1, int64_t a_s2,
                      float* H, int64_t h_s0, int64_t h_s1, int64_t h_s2, float* tau, int64_t tau_s0,
                      int64_t tau_s1, void* workspace, size_t workspace_bytes, void* stream_ptr) {

@@ -49,6 +49,12 @@ hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float
 hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n,
                             int k0, int nb, int slot0, int nwy, int c_begin, int c_end, bool vec, bool hi_prio,
                             int max_cus, hipStream_t stream, bool reverse = false);
+// The same transforms applied to a matrix C of its own (ormqr): V from the
+// first vcols columns of the factors (leading dimension ldv, m rows), C with
+// ccols columns (leading dimension ldc, m rows), every column of C updated.
+hipError_t launch_wy_apply(const float* V, int64_t batch, int64_t vs0, int64_t ldv, int vcols, float* C, int64_t cs0,
+                           int64_t ldc, int ccols, const float* Tws, int m, int k0, int nb, int slot0, int nwy,
+                           bool vec, hipStream_t stream, bool reverse);
 
 // Row-split compact-WY update (qr_update.hip): for tall matrices and small
 // batches the trailing update is split over row blocks as well as column
@@ -99,5 +105,14 @@ size_t orgqr_workspace_floats(int64_t batch, int n);
 hipError_t launch_orgqr(const float* H, int64_t batch, int n, int64_t hs0, int64_t hs1, int64_t hs2, const float* tau,
                         int64_t ts0, int64_t ts1, float* Q, int64_t qs0, int64_t ldq, float* ws, bool vec,
                         hipStream_t stream);
+
+// Q C or Q^T C in place in C (qr_orgqr.hip), Q = H_0 ... H_{r-1} from r
+// reflectors of m rows (H columns contiguous), C m x k (columns contiguous):
+// T of every 32-column panel, then the panels' transforms applied to C in
+// groups of kMaxWY (first to last for Q^T C, last to first for Q C).
+size_t ormqr_workspace_floats(int64_t batch, int r);
+hipError_t launch_ormqr(const float* H, int64_t batch, int m, int r, int64_t hs0, int64_t ldh, const float* tau,
+                        int64_t ts0, int64_t ts1, float* C, int64_t cs0, int64_t ldc, int k, bool transpose, float* ws,
+                        bool vec, hipStream_t stream);
 
 }  // namespace fastqr

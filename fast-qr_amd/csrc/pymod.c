@@ -3,7 +3,7 @@
  *
  * It only converts Python ints to the ABI's int64 / pointer arguments
  * (METH_FASTCALL, no argument tuples) and returns the status code; all
- * validation and every launch happen behind fastqr_geqrf_f32 / fastqr_orgqr_f32.  It exists so
+ * validation and every launch happen behind the fastqr_* entry points.  It exists so
  * that a call costs well under a microsecond of host time; ctypes over the
  * same library is equivalent and is what the tests use to check the ABI.
  */
@@ -64,6 +64,36 @@ static PyObject* py_orgqr(PyObject* self, PyObject* const* args, Py_ssize_t narg
   return PyLong_FromLong(rc);
 }
 
+/* ormqr(H, batch, m, r, hs0, hs1, hs2, tau, ts0, ts1, C, k, cs0, cs1, cs2, transpose, ws, ws_bytes, stream) -> int */
+static PyObject* py_ormqr(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
+  (void)self;
+  if (nargs != 19) {
+    PyErr_SetString(PyExc_TypeError, "ormqr expects 19 integer arguments");
+    return NULL;
+  }
+  void *H, *tau, *C, *ws, *stream;
+  int64_t b, m, r, hs0, hs1, hs2, ts0, ts1, k, cs0, cs1, cs2, tr, wsb;
+  if (as_ptr(args[0], &H) || as_i64(args[1], &b) || as_i64(args[2], &m) || as_i64(args[3], &r) ||
+      as_i64(args[4], &hs0) || as_i64(args[5], &hs1) || as_i64(args[6], &hs2) || as_ptr(args[7], &tau) ||
+      as_i64(args[8], &ts0) || as_i64(args[9], &ts1) || as_ptr(args[10], &C) || as_i64(args[11], &k) ||
+      as_i64(args[12], &cs0) || as_i64(args[13], &cs1) || as_i64(args[14], &cs2) || as_i64(args[15], &tr) ||
+      as_ptr(args[16], &ws) || as_i64(args[17], &wsb) || as_ptr(args[18], &stream))
+    return NULL;
+  const int rc = fastqr_ormqr_f32((const float*)H, b, m, r, hs0, hs1, hs2, (const float*)tau, ts0, ts1, (float*)C, k,
+                                  cs0, cs1, cs2, (int)tr, ws, (size_t)wsb, stream);
+  return PyLong_FromLong(rc);
+}
+
+static PyObject* py_ormqr_workspace_bytes(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
+  (void)self;
+  int64_t b, r;
+  if (nargs != 2 || as_i64(args[0], &b) || as_i64(args[1], &r)) {
+    if (!PyErr_Occurred()) PyErr_SetString(PyExc_TypeError, "ormqr_workspace_bytes(batch, r)");
+    return NULL;
+  }
+  return PyLong_FromSize_t(fastqr_ormqr_workspace_bytes(b, r));
+}
+
 static PyObject* py_orgqr_workspace_bytes(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
   (void)self;
   int64_t b, n;
@@ -109,6 +139,9 @@ static PyMethodDef methods[] = {
     {"orgqr", (PyCFunction)(void (*)(void))py_orgqr, METH_FASTCALL, "fastqr_orgqr_f32 over raw pointers"},
     {"orgqr_workspace_bytes", (PyCFunction)(void (*)(void))py_orgqr_workspace_bytes, METH_FASTCALL,
      "fastqr_orgqr_workspace_bytes"},
+    {"ormqr", (PyCFunction)(void (*)(void))py_ormqr, METH_FASTCALL, "fastqr_ormqr_f32 over raw pointers"},
+    {"ormqr_workspace_bytes", (PyCFunction)(void (*)(void))py_ormqr_workspace_bytes, METH_FASTCALL,
+     "fastqr_ormqr_workspace_bytes"},
     {"last_error", py_last_error, METH_NOARGS, "fastqr_last_error"},
     {"path_name", py_path_name, METH_O, "fastqr_path_name"},
     {"version", py_version, METH_NOARGS, "fastqr_version"},

@@ -121,8 +121,13 @@ __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __re
 // streams them twice.  Per transform: P = V^T X (the X registers are the B
 // operand, the contraction index permuted to match the accumulator layout),
 // P summed over waves in LDS, W = -(T^T P), X += V W.
-template <int NW, int TPW, bool RES, bool VEC>
-__device__ __forceinline__ void wy_update_item(float* __restrict__ H, int64_t hs0, int64_t ldh,
+//
+// SEPX: the updated columns live in a matrix X of their own (xcols columns,
+// leading dimension ldx, rows as H's) instead of H, and V is read from H's
+// first vcols columns (ormqr: Q C or Q^T C with V, T from a factorisation).
+template <int NW, int TPW, bool RES, bool VEC, bool SEPX>
+__device__ __forceinline__ void wy_update_item(float* __restrict__ H, int64_t hs0, int64_t ldh, int vcols,
+                                               float* __restrict__ X_, int64_t xs0, int64_t ldx, int xcols,
                                                const float* __restrict__ Tws, int n, int k0, int nb, int slot0,
                                                int nwy, int rev, int c_begin, int c_end, int64_t b, int strip) {
   const int lane = threadIdx.x & 63;
@@ -133,7 +138,9 @@ __device__ __forceinline__ void wy_update_item(float* __restrict__ H, int64_t hs
   const int ntiles = (m + 31) >> 5;
   const int col = c_begin + 32 * strip + l32;
   const bool colok = col < c_end;
-  const MatBuf M{make_rsrc(H + b * hs0, (uint32_t)(4 * ldh * n)), (int)ldh, n};
+  const MatBuf M{make_rsrc(H + b * hs0, (uint32_t)(4 * ldh * (SEPX ? vcols : n))), (int)ldh, n};
+  // the updated columns (H itself unless SEPX)
+  const MatBuf Mx = SEPX ? MatBuf{make_rsrc(X_ + b * xs0, (uint32_t)(4 * ldx * xcols)), (int)ldx, n} : M;
 
   __shared__ float Ts[kMaxWY][32][33];
   __shared__ float Pt[16][64];
@@ -156,7 +163,7 @@ __device__ __forceinline__ void wy_update_item(float* __restrict__ H, int64_t hs
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       const int rt = wave + NW * t;
-      X[t] = tile_load<VEC>(M, k0 + 32 * rt, col, colok && rt < ntiles, h);
+      X[t] = tile_load<VEC>(Mx, k0 + 32 * rt, col, colok && rt < ntiles, h);
     }
   }
   constexpr int kTChunk = 8;
@@ -221,7 +228,7 @@ __device__ __forceinline__ void wy_update_item(float* __restrict__ H, int64_t hs
     } else {
       for (int rt = wave; rt < ntiles; rt += NW) {
         if (rt < rt_first) continue;
-        const f32x16 Xs = tile_load<VEC>(M, k0 + 32 * rt, col, colok, h);
+        const f32x16 Xs = tile_load<VEC>(Mx, k0 + 32 * rt, col, colok, h);
         wy_accumulate<VEC>(P, Xs, M, kw, nb, k0 + 32 * rt, h, l32);
       }
     }
@@ -279,9 +286,9 @@ __device__ __forceinline__ void wy_update_item(float* __restrict__ H, int64_t hs
     } else {
       for (int rt = wave; rt < ntiles; rt += NW) {
         if (rt < rt_first) continue;
-        f32x16 C = tile_load<VEC>(M, k0 + 32 * rt, col, colok, h);
+        f32x16 C = tile_load<VEC>(Mx, k0 + 32 * rt, col, colok, h);
         wy_apply(C, W, M, kw, nb, k0 + 32 * rt, h, l32);
-        tile_store<VEC>(M, k0 + 32 * rt, col, colok, h, C);
+        tile_store<VEC>(Mx, k0 + 32 * rt, col, colok, h, C);
       }
       // the next transform reloads what this wave stored
       __syncthreads();
@@ -295,7 +302,7 @@ __device__ __forceinline__ void wy_update_item(float* __restrict__ H, int64_t hs
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       const int rt = wave + NW * t;
-      tile_store<VEC>(M, kb + 32 * rt, cs, colok && rt < ntiles, h, X[t]);
+      tile_store<VEC>(Mx, kb + 32 * rt, cs, colok && rt < ntiles, h, X[t]);
     }
   }
 }
@@ -308,11 +315,12 @@ __device__ __forceinline__ void wy_update_item(float* __restrict__ H, int64_t hs
 // than the item count loops (stride a multiple of 8, so each workgroup stays
 // on its XCD's matrices): the caller uses it to leave CUs free for the
 // critical-path kernels on the other stream.
-template <int NW, int TPW, bool RES, bool VEC>
+template <int NW, int TPW, bool RES, bool VEC, bool SEPX>
 __global__ void __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu((TPW >= 2 && NW >= 4) || (TPW >= 4 && NW <= 4) ? 2 : 4, 8)))
-wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* __restrict__ Tws, int n, int k0,
-                 int nb, int slot0, int nwy, int rev, int c_begin, int c_end, int hi_prio, int nstrips, int batch) {
+wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, int vcols, float* __restrict__ X, int64_t xs0,
+                 int64_t ldx, int xcols, const float* __restrict__ Tws, int n, int k0, int nb, int slot0, int nwy,
+                 int rev, int c_begin, int c_end, int hi_prio, int nstrips, int batch) {
   // updates on the critical path (the rest of a panel group, the next group's
   // columns) win issue arbitration against the wide update they overlap
   if (hi_prio) __builtin_amdgcn_s_setprio(2);
@@ -321,7 +329,9 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, const float* _
     const int xk = L >> 3;
     const int64_t b = (L & 7) + 8 * (xk / nstrips);
     const int strip = xk % nstrips;
-    if (b < batch) wy_update_item<NW, TPW, RES, VEC>(H, hs0, ldh, Tws, n, k0, nb, slot0, nwy, rev, c_begin, c_end, b, strip);
+    if (b < batch)
+      wy_update_item<NW, TPW, RES, VEC, SEPX>(H, hs0, ldh, vcols, X, xs0, ldx, xcols, Tws, n, k0, nb, slot0, nwy, rev,
+                                              c_begin, c_end, b, strip);
     __syncthreads();  // the next item rewrites the LDS buffers
   }
 }
@@ -368,9 +378,13 @@ int wgs_per_cu(K kernel, int threads) {
 
 }  // namespace
 
-hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n,
-                            int k0, int nb, int slot0, int nwy, int c_begin, int c_end, bool vec, bool hi_prio,
-                            int max_cus, hipStream_t stream, bool reverse) {
+// Shared by launch_wy_update (X = H) and launch_wy_apply (X a matrix of its
+// own, SEPX): picks the (waves, tiles per wave) variant and the grid.
+template <bool SEPX>
+static hipError_t launch_wy(float* H, int64_t batch, int64_t hs0, int64_t ldh, int vcols, float* X, int64_t xs0,
+                            int64_t ldx, int xcols, const float* Tws, int n, int k0, int nb, int slot0, int nwy,
+                            int c_begin, int c_end, bool vec, bool hi_prio, int max_cus, hipStream_t stream,
+                            bool reverse) {
   const int cols = c_end - c_begin;
   if (cols <= 0 || nwy <= 0) return hipSuccess;
   const int ntiles = (n - k0 + 31) / 32;
@@ -416,16 +430,15 @@ hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, c
   const bool res = nw * tpw >= ntiles;
   const int prio = hi_prio ? 1 : 0;
   const int rv = reverse ? 1 : 0;
-#define FASTQR_WY(NW, TPW, RES)                                                                                 \
-  if (nw == NW && tpw == TPW && res == RES) {                                                                   \
-    if (vec)                                                                                                    \
-      hipLaunchKernelGGL((wy_update_kernel<NW, TPW, RES, true>), grid_for(wy_update_kernel<NW, TPW, RES, true>, NW * 64), dim3(NW * 64), 0, stream, H, hs0, ldh,    \
-                         Tws, n, k0, nb, slot0, nwy, rv, c_begin, c_end, prio, ns, nbatch);                                     \
-    else                                                                                                        \
-      hipLaunchKernelGGL((wy_update_kernel<NW, TPW, RES, false>), grid_for(wy_update_kernel<NW, TPW, RES, false>, NW * 64), dim3(NW * 64), 0, stream, H, hs0, ldh,   \
-                         Tws, n, k0, nb, slot0, nwy, rv, c_begin, c_end, prio, ns, nbatch);                                     \
-    return hipGetLastError();                                                                                   \
-  }
+  auto go = [&](auto kernel, int threads) -> hipError_t {
+    hipLaunchKernelGGL(kernel, grid_for(kernel, threads), dim3(threads), 0, stream, H, hs0, ldh, vcols, X, xs0, ldx,
+                       xcols, Tws, n, k0, nb, slot0, nwy, rv, c_begin, c_end, prio, ns, nbatch);
+    return hipGetLastError();
+  };
+#define FASTQR_WY(NW, TPW, RES)                                                                     \
+  if (nw == NW && tpw == TPW && res == RES)                                                         \
+    return vec ? go(wy_update_kernel<NW, TPW, RES, true, SEPX>, NW * 64)                            \
+               : go(wy_update_kernel<NW, TPW, RES, false, SEPX>, NW * 64);
   FASTQR_WY(1, 1, true)
   FASTQR_WY(2, 1, true)
   FASTQR_WY(4, 1, true)
@@ -441,13 +454,21 @@ hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, c
   FASTQR_WY(8, 8, true)
 #undef FASTQR_WY
   // strips taller than 8 waves x 8 tiles: stream the tiles
-  if (vec)
-    hipLaunchKernelGGL((wy_update_kernel<16, 1, false, true>), grid_for(wy_update_kernel<16, 1, false, true>, 1024), dim3(16 * 64), 0, stream, H, hs0, ldh, Tws, n,
-                       k0, nb, slot0, nwy, rv, c_begin, c_end, prio, ns, nbatch);
-  else
-    hipLaunchKernelGGL((wy_update_kernel<16, 1, false, false>), grid_for(wy_update_kernel<16, 1, false, false>, 1024), dim3(16 * 64), 0, stream, H, hs0, ldh, Tws, n,
-                       k0, nb, slot0, nwy, rv, c_begin, c_end, prio, ns, nbatch);
-  return hipGetLastError();
+  return vec ? go(wy_update_kernel<16, 1, false, true, SEPX>, 1024) : go(wy_update_kernel<16, 1, false, false, SEPX>, 1024);
+}
+
+hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n,
+                            int k0, int nb, int slot0, int nwy, int c_begin, int c_end, bool vec, bool hi_prio,
+                            int max_cus, hipStream_t stream, bool reverse) {
+  return launch_wy<false>(H, batch, hs0, ldh, n, H, hs0, ldh, n, Tws, n, k0, nb, slot0, nwy, c_begin, c_end, vec,
+                          hi_prio, max_cus, stream, reverse);
+}
+
+hipError_t launch_wy_apply(const float* V, int64_t batch, int64_t vs0, int64_t ldv, int vcols, float* C, int64_t cs0,
+                           int64_t ldc, int ccols, const float* Tws, int m, int k0, int nb, int slot0, int nwy,
+                           bool vec, hipStream_t stream, bool reverse) {
+  return launch_wy<true>(const_cast<float*>(V), batch, vs0, ldv, vcols, C, cs0, ldc, ccols, Tws, m, k0, nb, slot0,
+                         nwy, 0, ccols, vec, false, 0, stream, reverse);
 }
 
 }  // namespace fastqr

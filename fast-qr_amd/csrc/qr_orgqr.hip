@@ -40,15 +40,17 @@ __global__ void __launch_bounds__(256) orgqr_init_kernel(const float* __restrict
 // v_mfma_f32_32x32x2f32: for rows (r, r+1) lane (h, c) holds V(r+h, c), which
 // is both its A element (V^T) and its B element (V).  The slarft recurrence
 // T(i, j) = -tau_j sum_{i <= l < j} T(i, l) G(l, j) needs only row i of T, so
-// lane i runs it alone.
+// lane i runs it alone.  The panel's reflectors are columns k0.. of the first
+// nrefl (rows k0..n).  t_trans: store T^T (orgqr) or T itself (ormqr's Q^T C);
+// Y is formed only when Yws is given.
 __global__ void __launch_bounds__(256) orgqr_larft_kernel(const float* __restrict__ Q, int64_t qs0, int ldq, int n,
-                                                          const float* __restrict__ tau, int64_t ts0, int64_t ts1,
-                                                          int64_t batch, float* __restrict__ Tws,
-                                                          float* __restrict__ Yws) {
+                                                          int nrefl, const float* __restrict__ tau, int64_t ts0,
+                                                          int64_t ts1, int64_t batch, float* __restrict__ Tws,
+                                                          float* __restrict__ Yws, int t_trans) {
   const int p = blockIdx.x;
   const int64_t b = blockIdx.y;
   const int k0 = 32 * p;
-  const int nb = min(32, n - k0);
+  const int nb = min(32, nrefl - k0);
   const int m = n - k0;
   const float* Qb = Q + b * qs0;
   const int t = threadIdx.x;
@@ -133,13 +135,20 @@ __global__ void __launch_bounds__(256) orgqr_larft_kernel(const float* __restric
   }
   __syncthreads();
 
-  float* To = Tws + (((int64_t)(p / kMaxSlots) * batch + b) * kMaxSlots + (p % kMaxSlots)) * 1024;
-  float* Yo = Yws + (((int64_t)(p / kMaxSlots) * batch + b) * kMaxSlots + (p % kMaxSlots)) * 1024;
+  const int64_t slot = ((int64_t)(p / kMaxSlots) * batch + b) * kMaxSlots + (p % kMaxSlots);
+  float* To = Tws + slot * 1024;
 #pragma unroll
   for (int u = 0; u < 4; ++u) {
     const int idx = t + 256 * u;
     const int r = idx >> 5, c = idx & 31;
-    To[idx] = Ts[c][r];
+    To[idx] = t_trans ? Ts[c][r] : Ts[r][c];
+  }
+  if (Yws == nullptr) return;
+  float* Yo = Yws + slot * 1024;
+#pragma unroll
+  for (int u = 0; u < 4; ++u) {
+    const int idx = t + 256 * u;
+    const int r = idx >> 5, c = idx & 31;
     // Y(r, c) = sum_l T(r, l) V1(c, l): T is zero left of its diagonal and V1
     // (staged with its unit diagonal and zeros) right of its own
     float y = 0.0f;
@@ -275,7 +284,7 @@ hipError_t launch_orgqr(const float* H, int64_t batch, int n, int64_t hs0, int64
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(orgqr_larft_kernel, dim3((unsigned)npan, (unsigned)batch), dim3(256), 0, stream, Q, qs0,
-                     (int)ldq, n, tau, ts0, ts1, batch, Tws, Yws);
+                     (int)ldq, n, n, tau, ts0, ts1, batch, Tws, Yws, 1);
   if ((e = hipGetLastError()) != hipSuccess) return e;
 
   auto panel_q = [&](int p) -> hipError_t {
@@ -384,6 +393,41 @@ hipError_t launch_orgqr(const float* H, int64_t batch, int n, int64_t hs0, int64
       }
       if ((e = panel_q(p)) != hipSuccess) return e;
     }
+  }
+  return hipSuccess;
+}
+
+size_t ormqr_workspace_floats(int64_t batch, int r) {
+  const int64_t npan = (r + 31) / 32;
+  const int64_t nchunk = (npan + kMaxSlots - 1) / kMaxSlots;
+  return (size_t)(nchunk * batch * kMaxSlots * 1024);
+}
+
+// LAPACK sormqr (SIDE = 'L') in compact-WY form, as the blocked geqrf applies
+// a panel group: T of every 32-column panel in one orgqr_larft_kernel launch
+// (stored as T for Q^T C, whose blocks B_p^T = I - V T^T V^T are what the
+// update kernels apply with a stored T, and as T^T for Q C, whose blocks are
+// B_p = I - V T V^T), then one strip-resident update of every column of C per
+// group of kMaxWY panels: C is loaded and stored once per group.
+hipError_t launch_ormqr(const float* H, int64_t batch, int m, int r, int64_t hs0, int64_t ldh, const float* tau,
+                        int64_t ts0, int64_t ts1, float* C, int64_t cs0, int64_t ldc, int k, bool transpose, float* ws,
+                        bool vec, hipStream_t stream) {
+  if (r <= 0 || k <= 0) return hipSuccess;
+  const int npan = (r + 31) / 32;
+  hipLaunchKernelGGL(orgqr_larft_kernel, dim3((unsigned)npan, (unsigned)batch), dim3(256), 0, stream, H, hs0, (int)ldh,
+                     m, r, tau, ts0, ts1, batch, ws, nullptr, transpose ? 0 : 1);
+  hipError_t e = hipGetLastError();
+  if (e != hipSuccess) return e;
+  static_assert(kMaxSlots % kMaxWY == 0, "a panel group must not straddle two T chunks");
+  const int ngroups = (npan + kMaxWY - 1) / kMaxWY;
+  for (int s = 0; s < ngroups; ++s) {
+    const int g = transpose ? s : ngroups - 1 - s;  // Q^T C: H_0 first; Q C: H_{r-1} first
+    const int p0 = kMaxWY * g;
+    const int p1 = min(p0 + kMaxWY, npan);
+    const float* Tchunk = ws + (int64_t)(p0 / kMaxSlots) * batch * kMaxSlots * 1024;
+    e = launch_wy_apply(H, batch, hs0, ldh, r, C, cs0, ldc, k, Tchunk, m, 32 * p0, 32, p0 % kMaxSlots, p1 - p0, vec,
+                        stream, /*reverse=*/!transpose);
+    if (e != hipSuccess) return e;
   }
   return hipSuccess;
 }

@@ -32,6 +32,8 @@ EXPORTED_SYMBOLS = (
     "fastqr_workspace_bytes",
     "fastqr_orgqr_f32",
     "fastqr_orgqr_workspace_bytes",
+    "fastqr_ormqr_f32",
+    "fastqr_ormqr_workspace_bytes",
     "fastqr_path_name",
     "fastqr_last_error",
     "fastqr_version",
@@ -82,6 +84,11 @@ def cdll() -> ctypes.CDLL:
         lib.fastqr_orgqr_f32.restype = ctypes.c_int
         lib.fastqr_orgqr_workspace_bytes.argtypes = [i64, i64]
         lib.fastqr_orgqr_workspace_bytes.restype = sz
+        lib.fastqr_ormqr_f32.argtypes = [vp, i64, i64, i64, i64, i64, i64, vp, i64, i64, vp, i64, i64, i64, i64,
+                                         ctypes.c_int, vp, sz, vp]
+        lib.fastqr_ormqr_f32.restype = ctypes.c_int
+        lib.fastqr_ormqr_workspace_bytes.argtypes = [i64, i64]
+        lib.fastqr_ormqr_workspace_bytes.restype = sz
         lib.fastqr_workspace_bytes.restype = sz
         lib.fastqr_path_name.argtypes = [i64]
         lib.fastqr_path_name.restype = ctypes.c_char_p

@@ -63,18 +63,48 @@ def householder_product(h: torch.Tensor, tau: torch.Tensor, *, out: torch.Tensor
 
 
 def apply_q(h: torch.Tensor, tau: torch.Tensor, c: torch.Tensor, *, transpose: bool = False) -> torch.Tensor:
-    """Q C (or Q^T C with ``transpose``) for the geqrf factors ``(h, tau)``.
+    """Q C (or Q^T C with ``transpose``) for geqrf factors ``(h, tau)``, without forming Q.
 
     The meaning of ``torch.ormqr(h, tau, c, left=True, transpose=transpose)``
-    for square h with n reflectors and C of shape (batch, n, k): Q is formed
-    by ``householder_product`` (the HIP kernels) and applied with one batched
-    fp32 GEMM (``torch.bmm``, hipBLAS), a plain library product.
+    (the reference's call on geqrf factors, submissions/candidate.py:7231-7237):
+    ``h`` is (batch, m, r) with r <= m reflectors below its diagonal, ``tau``
+    (batch, r), ``c`` (batch, m, k).  One call into the gfx950 C ABI
+    (``fastqr_ormqr_f32``): the compact-WY transforms of every 32-column panel
+    applied to a column-major copy of C by the MFMA update kernels.  Returns a
+    new tensor (column-major, like geqrf's H); ``c`` is not modified.
     """
-    b, n = _check(h, tau)
-    if not isinstance(c, torch.Tensor) or c.dtype != torch.float32 or c.device != h.device:
-        raise TypeError("c must be a float32 tensor on h's device")
-    if c.dim() != 3 or c.shape[0] != b or c.shape[1] != n:
-        raise ValueError(f"c must have shape ({b}, {n}, k), got {tuple(c.shape)}")
-    q = householder_product(h, tau)
-    qm = q.transpose(-1, -2) if transpose else q
-    return torch.bmm(qm.contiguous(), c.contiguous())
+    if not isinstance(h, torch.Tensor) or not isinstance(tau, torch.Tensor) or not isinstance(c, torch.Tensor):
+        raise TypeError("h, tau and c must be torch.Tensors")
+    if h.dtype != torch.float32 or tau.dtype != torch.float32 or c.dtype != torch.float32:
+        raise TypeError("h, tau and c must be float32")
+    if h.dim() != 3 or h.shape[2] > h.shape[1]:
+        raise ValueError(f"h must have shape (batch, m, r) with r <= m, got {tuple(h.shape)}")
+    b, m, r = h.shape
+    if tuple(tau.shape) != (b, r):
+        raise ValueError(f"tau must have shape {(b, r)}, got {tuple(tau.shape)}")
+    if c.dim() != 3 or c.shape[0] != b or c.shape[1] != m:
+        raise ValueError(f"c must have shape ({b}, {m}, k), got {tuple(c.shape)}")
+    if not h.is_cuda or tau.device != h.device or c.device != h.device:
+        raise ValueError("h, tau and c must be CUDA (HIP) tensors on one device")
+    idx = h.get_device()
+    if idx != torch.cuda.current_device():
+        with torch.cuda.device(idx):
+            return apply_q(h, tau, c, transpose=transpose)
+    k = c.shape[2]
+    out = torch.empty_strided((b, m, k), (m * k, 1, m), dtype=torch.float32, device=h.device)
+    out.copy_(c)
+    if b == 0 or m == 0 or k == 0 or r == 0:
+        return out
+    if h.stride(1) != 1 or h.stride(2) < m:  # the kernels read V in column segments
+        h = h.transpose(-1, -2).contiguous().transpose(-1, -2)
+    mod = ext()
+    sptr = _current_stream_ptr(idx)
+    ws = workspace.scratch(h.device, sptr, mod.ormqr_workspace_bytes(b, r))
+    hs0, hs1, hs2 = h.stride()
+    ts0, ts1 = tau.stride()
+    cs0, cs1, cs2 = out.stride()
+    rc = mod.ormqr(h.data_ptr(), b, m, r, hs0, hs1, hs2, tau.data_ptr(), ts0, ts1, out.data_ptr(), k, cs0, cs1, cs2,
+                   1 if transpose else 0, 0 if ws is None else ws.data_ptr(), 0 if ws is None else ws.numel(), sptr)
+    if rc != 0:
+        raise FastQRError(rc, mod.last_error())
+    return out

@@ -139,6 +139,39 @@ int fastqr_orgqr_f32(const float* H, int64_t batch, int64_t n,
 size_t fastqr_orgqr_workspace_bytes(int64_t batch, int64_t n);
 
 /*
+ * Q C or Q^T C for batched compact-Householder factors, in place in C
+ * (LAPACK sormqr with SIDE = 'L'), without forming Q: Q = H_0 H_1 ... H_{r-1},
+ * H_k = I - tau[k] v_k v_k^T.  Replaces torch.ormqr(H, tau, C, left=True,
+ * transpose=...), the call the reference makes on geqrf factors
+ * (submissions/candidate.py:7231-7237).
+ *
+ * H      device pointer to (batch, m, r) factors, r <= m: element (b, i, j)
+ *        at H[b*h_s0 + i*h_s1 + j*h_s2], columns contiguous (h_s1 == 1,
+ *        h_s2 >= m); only the strictly lower part is read.
+ * tau    device pointer, element (b, j) at tau[b*tau_s0 + j*tau_s1], j < r.
+ * C      device pointer to (batch, m, k): element (b, i, j) at
+ *        C[b*c_s0 + i*c_s1 + j*c_s2], columns contiguous (c_s1 == 1,
+ *        c_s2 >= m); overwritten by Q C (transpose == 0) or Q^T C (!= 0).
+ *        C must not overlap H or tau.
+ * workspace / workspace_bytes  at least fastqr_ormqr_workspace_bytes(batch, r)
+ *        bytes of device scratch, 16-byte aligned (T of every 32-column panel);
+ *        may be NULL when that size is 0.
+ * stream a hipStream_t; asynchronous, no host synchronisation.
+ *
+ * 1 <= m <= 4096.  Returns FASTQR_OK, a negative FASTQR_E* argument error, or
+ * a positive hipError_t if a launch failed.
+ */
+int fastqr_ormqr_f32(const float* H, int64_t batch, int64_t m, int64_t r,
+                     int64_t h_s0, int64_t h_s1, int64_t h_s2,
+                     const float* tau, int64_t tau_s0, int64_t tau_s1,
+                     float* C, int64_t k, int64_t c_s0, int64_t c_s1, int64_t c_s2,
+                     int transpose, void* workspace, size_t workspace_bytes,
+                     void* stream);
+
+/* Workspace bytes fastqr_ormqr_f32 needs for (batch, r). */
+size_t fastqr_ormqr_workspace_bytes(int64_t batch, int64_t r);
+
+/*
  * Name of the kernel path fastqr_geqrf_f32 takes for size n ("wave64",
  * "lds", "blocked"); the reference's shape switch is custom_kernel
  * (submissions/candidate.py:8383-8415).  Never NULL.
@@ -154,8 +187,8 @@ const char* fastqr_last_error(void);
 int fastqr_version(void);
 
 /*
- * Test hook: when `code` is non-zero the next fastqr_geqrf_f32 or
- * fastqr_orgqr_f32 call on this thread returns `code` without launching
+ * Test hook: when `code` is non-zero the next fastqr_geqrf_f32,
+ * fastqr_orgqr_f32 or fastqr_ormqr_f32 call on this thread returns `code` without launching
  * anything (used to test the host's error path without faulting a GPU).  No
  * counterpart in the reference.
  */

@@ -119,26 +119,86 @@ def test_full_workload_q_reconstructs_input(cuda, name, idx):
     assert orth.max().item() <= 1e-5 * n
 
 
-# Q C and Q^T C (torch.ormqr's meaning) against the oracle: CPU torch.ormqr in
-# fp64 on the same factors; tolerance ||X - X_ref||_F <= 1e-5 n ||C||_F.
-@pytest.mark.parametrize("batch,n,k,transpose", [(3, 20, 5, False), (3, 100, 100, True), (2, 600, 7, True),
-                                                 (2, 600, 7, False)])
-def test_apply_q_matches_ormqr(cuda, batch, n, k, transpose):
-    _say(f"[apply_q] batch={batch} n={n} k={k} transpose={transpose}")
-    a = gaussian(batch, n, 300 + n)
-    cm = gaussian(batch, max(n, k), 301 + n)[:, :n, :k].contiguous()
-    h, tau = custom_kernel(a.to(cuda))
-    x = fastqr.apply_q(h, tau, cm.to(cuda), transpose=transpose)
+# Q C and Q^T C (torch.ormqr's meaning, fastqr.apply_q over the C ABI
+# fastqr_ormqr_f32) against the oracle: CPU torch.ormqr in fp64 on the same
+# factors; tolerance ||X - X_ref||_F <= 1e-5 n ||C||_F.  Square factors come
+# from custom_kernel; rectangular (m x r) ones, as the reference's call on a
+# leading column block (submissions/candidate.py:7231-7237), from CPU geqrf.
+# The shapes cover one and several panel groups, r not a multiple of 32 (a
+# partial last panel and group), k of 1 and not a multiple of 32, m not a
+# multiple of 4 (element loads), and strips taller than 2048 rows (the
+# streaming form of the update kernel).
+@pytest.mark.parametrize("batch,m,r,k,transpose", [
+    (3, 20, 20, 5, False), (3, 100, 100, 100, True), (2, 600, 600, 7, True), (2, 600, 600, 7, False),
+    (2, 512, 512, 512, False), (2, 512, 512, 512, True), (4, 300, 77, 45, False), (4, 300, 77, 45, True),
+    (3, 333, 333, 1, True), (2, 333, 200, 70, False), (1, 2100, 2100, 33, True), (1, 2100, 2100, 33, False),
+    (1, 4096, 4096, 40, False)])
+def test_apply_q_matches_ormqr(cuda, batch, m, r, k, transpose):
+    _say(f"[apply_q] batch={batch} m={m} r={r} k={k} transpose={transpose}")
+    g = torch.Generator().manual_seed(300 + m + r)
+    cm = torch.randn((batch, m, k), generator=g, dtype=torch.float32)
+    if r == m:
+        h, tau = custom_kernel(gaussian(batch, m, 300 + m).to(cuda))
+    else:
+        h, tau = torch.geqrf(torch.randn((batch, m, r), generator=g, dtype=torch.float32))
+        h, tau = h.to(cuda), tau.to(cuda)
+    c_dev = cm.to(cuda)
+    x = fastqr.apply_q(h, tau, c_dev, transpose=transpose)
     torch.cuda.synchronize()
+    assert torch.equal(c_dev.cpu(), cm)  # C itself is not modified
     x_ref = torch.ormqr(h.cpu().double(), tau.cpu().double(), cm.double(), left=True, transpose=transpose)
     err = (torch.linalg.matrix_norm(x.cpu().double() - x_ref) / torch.linalg.matrix_norm(cm.double())).max().item()
-    assert err <= 1e-5 * n, f"||X - X_ref||_F / ||C||_F = {err:.3e}"
-    # Q^T (Q C) = C
-    if transpose:
-        back = fastqr.apply_q(h, tau, x, transpose=False)
-        torch.cuda.synchronize()
-        assert (torch.linalg.matrix_norm((back.cpu() - cm).double()) /
-                torch.linalg.matrix_norm(cm.double())).max().item() <= 1e-5 * n
+    _say(f"  ||X - X_ref||_F / ||C||_F = {err:.2e}")
+    assert err <= 1e-5 * m, f"||X - X_ref||_F / ||C||_F = {err:.3e}"
+    # Q^T (Q C) = C and Q (Q^T C) = C
+    back = fastqr.apply_q(h, tau, x, transpose=not transpose)
+    torch.cuda.synchronize()
+    assert (torch.linalg.matrix_norm((back.cpu() - cm).double()) /
+            torch.linalg.matrix_norm(cm.double())).max().item() <= 1e-5 * m
+
+
+def test_apply_q_equals_explicit_q_product(cuda):
+    """Q C by the compact-WY path against the explicit Q (householder_product)
+    times C in fp64: two different kernel paths over the same factors."""
+    a = gaussian(4, 384, 77)
+    h, tau = custom_kernel(a.to(cuda))
+    c = torch.randn((4, 384, 96), generator=torch.Generator().manual_seed(78))
+    x = fastqr.apply_q(h, tau, c.to(cuda))
+    q = fastqr.householder_product(h, tau)
+    torch.cuda.synchronize()
+    ref = q.cpu().double() @ c.double()
+    err = (torch.linalg.matrix_norm(x.cpu().double() - ref) / torch.linalg.matrix_norm(c.double())).max().item()
+    assert err <= 1e-5 * 384, err
+
+
+def test_ormqr_c_abi_with_padded_c(cuda):
+    """fastqr_ormqr_f32 through ctypes on a C with padded columns (leading
+    dimension m + 3: element loads) and a batch stride beyond one matrix;
+    the padding is left untouched."""
+    import ctypes
+
+    b, m, k = 3, 200, 50
+    a = gaussian(b, m, 91)
+    h, tau = custom_kernel(a.to(cuda))
+    ldc = m + 3
+    cbuf = torch.randn((b, k + 1, ldc), generator=torch.Generator().manual_seed(92)).to(cuda)
+    cview = cbuf[:, :k, :m].transpose(-1, -2)  # (b, m, k), strides (ldc*(k+1), 1, ldc)
+    c_ref = torch.ormqr(h.cpu().double(), tau.cpu().double(), cview.cpu().double(), left=True, transpose=True)
+    before = cbuf.cpu()
+    lib = fastqr.cdll()
+    nbytes = lib.fastqr_ormqr_workspace_bytes(b, m)
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=cuda)
+    torch.cuda.synchronize()
+    rc = lib.fastqr_ormqr_f32(h.data_ptr(), b, m, m, *h.stride(), tau.data_ptr(), *tau.stride(), cview.data_ptr(), k,
+                              *cview.stride(), 1, ws.data_ptr(), nbytes, 0)
+    torch.cuda.synchronize()
+    assert rc == 0, lib.fastqr_last_error()
+    after = cbuf.cpu()
+    err = (torch.linalg.matrix_norm(after[:, :k, :m].transpose(-1, -2).double() - c_ref) /
+           torch.linalg.matrix_norm(before[:, :k, :m].double())).max().item()
+    assert err <= 1e-5 * m, err
+    assert torch.equal(after[:, :k, m:], before[:, :k, m:])  # row padding
+    assert torch.equal(after[:, k:, :], before[:, k:, :])    # the extra column
 
 
 def test_forced_error_in_householder_product_surfaces(cuda):

@@ -264,6 +264,45 @@ def test_orgqr_argument_validation_returns_codes_without_launching():
     assert _orgqr_call(lib) == -99
 
 
+def _ormqr_call(lib, H=8, b=2, m=100, r=100, h_s=None, tau=32, t_s=None, C=16, k=40, c_s=None, tr=1, ws=64,
+                ws_bytes=1 << 30):
+    h_s0, h_s1, h_s2 = (m * r, 1, m) if h_s is None else h_s
+    c_s0, c_s1, c_s2 = (m * k, 1, m) if c_s is None else c_s
+    t_s0, t_s1 = (r, 1) if t_s is None else t_s
+    base = 1 << 40  # fake, never-dereferenced addresses (validation only)
+    return lib.fastqr_ormqr_f32(base * H if H else None, b, m, r, h_s0, h_s1, h_s2, base * tau if tau else None,
+                                t_s0, t_s1, base * C if C else None, k, c_s0, c_s1, c_s2, tr,
+                                base * ws if ws else None, ws_bytes, None)
+
+
+def test_ormqr_argument_validation_returns_codes_without_launching():
+    lib = fastqr.cdll()
+    assert lib.fastqr_ormqr_workspace_bytes(0, 64) == 0
+    assert lib.fastqr_ormqr_workspace_bytes(2, 0) == 0
+    one = lib.fastqr_ormqr_workspace_bytes(1, 512)
+    assert one >= 16 * 32 * 32 * 4 and one % 256 == 0  # a T factor per 32-column panel
+    assert lib.fastqr_ormqr_workspace_bytes(640, 512) >= 640 * one - 255
+    # nothing to do: empty batch, no rows, no columns of C, no reflectors (Q = I)
+    for kw in ({"b": 0}, {"m": 0, "r": 0}, {"k": 0}, {"r": 0}):
+        assert _ormqr_call(lib, **kw) == _lib.FASTQR_OK
+    assert _ormqr_call(lib, r=101) == _lib.FASTQR_EINVAL  # more reflectors than rows
+    assert b"exceed" in lib.fastqr_last_error()
+    assert _ormqr_call(lib, m=5000, r=10) == _lib.FASTQR_EINVAL
+    assert _ormqr_call(lib, k=-1) == _lib.FASTQR_EINVAL
+    assert _ormqr_call(lib, C=0) == _lib.FASTQR_EINVAL
+    assert b"non-null" in lib.fastqr_last_error()
+    assert _ormqr_call(lib, c_s=(4000, 40, 1)) == _lib.FASTQR_ELAYOUT  # row-major C
+    assert b"C must have contiguous columns" in lib.fastqr_last_error()
+    assert _ormqr_call(lib, h_s=(10000, 100, 1)) == _lib.FASTQR_ELAYOUT  # row-major H
+    assert _ormqr_call(lib, c_s=(10, 1, 100)) == _lib.FASTQR_ELAYOUT  # batch stride inside a matrix
+    assert _ormqr_call(lib, ws_bytes=16) == _lib.FASTQR_EWORKSPACE
+    assert _ormqr_call(lib, ws=0) == _lib.FASTQR_EWORKSPACE
+    assert _ormqr_call(lib, C=8) == _lib.FASTQR_EOVERLAP  # C on top of H
+    assert _ormqr_call(lib, tau=16) == _lib.FASTQR_EOVERLAP  # tau inside C
+    lib.fastqr_debug_force_error(-99)
+    assert _ormqr_call(lib) == -99
+
+
 def test_householder_product_rejects_bad_inputs_loudly():
     h = torch.zeros((2, 8, 8))
     with pytest.raises(ValueError):
@@ -280,6 +319,12 @@ def test_apply_q_rejects_bad_inputs_loudly():
     h = torch.zeros((2, 8, 8))
     with pytest.raises(ValueError):
         fastqr.apply_q(h, torch.zeros((2, 8)), torch.zeros((2, 8, 3)))  # CPU tensors
+    with pytest.raises(ValueError):
+        fastqr.apply_q(torch.zeros((2, 8, 9)), torch.zeros((2, 9)), torch.zeros((2, 8, 3)))  # r > m
+    with pytest.raises(ValueError):
+        fastqr.apply_q(h, torch.zeros((2, 8)), torch.zeros((2, 7, 3)))  # C rows
+    with pytest.raises(TypeError):
+        fastqr.apply_q(h, torch.zeros((2, 8)), torch.zeros((2, 8, 3), dtype=torch.float64))
 
 
 def test_missing_native_library_fails_loudly(monkeypatch, tmp_path):
