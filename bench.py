@@ -14,9 +14,12 @@ mean of microseconds per custom_kernel call over the five benchmark workloads
 Timing follows official/eval.py:157-222: per shape, `count` distinct inputs
 (count = clamp(256 MiB / input bytes, 1, 50), seed += 42 per input), a cache
 flush before every repeat (1 GiB here, as MI355X has a 256 MB Infinity Cache),
-HIP events around the `count` calls on torch's current stream, and a recheck
-of the outputs after the timed region.  One step = one such repeat of every
-shape.  A second, instrumented pass records per-kernel HIP events inside the
+a synchronize before and after every repeat, HIP events around the `count`
+calls on torch's current stream, and a recheck of the outputs after the timed
+region.  As in the evaluator, each shape's repeats run back to back and the
+shapes follow one another (a shape never starts right behind another shape's
+repeat, whose MFMA load leaves the clock lower for the next few
+milliseconds).  One step = one repeat of every shape.  A second, instrumented pass records per-kernel HIP events inside the
 library (fastqr_profile_*) to give each kernel's average launch duration and
 its roofline fraction.  CPU torch.geqrf (the reference's own path) is timed
 on this host's cores on a bounded sample of each shape.
@@ -505,23 +508,24 @@ def main() -> int:
     torch.cuda.synchronize()
 
     # ---- timed region ---------------------------------------------------------
+    # shape-major with a synchronize around every repeat, as the evaluator runs
+    # each case (official/eval.py:196-207)
     per_shape_us = {s.label: [] for _, s in shapes}
-    events = []
     torch.cuda.synchronize()
     wall0 = time.perf_counter()
-    for _ in range(args.steps):
-        for _, s in shapes:
+    for _, s in shapes:
+        for _ in range(args.steps):
+            torch.cuda.synchronize()
             flush_buf.fill_(42)
             e0 = torch.cuda.Event(enable_timing=True)
             e1 = torch.cuda.Event(enable_timing=True)
             e0.record()
             outs = run_shape(s.label)
             e1.record()
-            events.append((s.label, e0, e1, len(outs)))
+            torch.cuda.synchronize()
+            per_shape_us[s.label].append(e0.elapsed_time(e1) * 1e3 / len(outs))
     torch.cuda.synchronize()
     wall = time.perf_counter() - wall0
-    for label, e0, e1, cnt in events:
-        per_shape_us[label].append(e0.elapsed_time(e1) * 1e3 / cnt)
 
     # ---- C2 with column-major inputs (the layout BASELINE C2 names): the same
     # values as column-major views, timed like the headline shapes ----------------
