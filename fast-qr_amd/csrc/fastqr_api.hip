@@ -678,10 +678,10 @@ int fastqr_orgqr_f32(const float* H, int64_t batch, int64_t n, int64_t h_s0, int
   return FASTQR_OK;
 }
 
-size_t fastqr_ormqr_workspace_bytes(int64_t batch, int64_t r) {
-  if (batch <= 0 || r <= 0 || r > kMaxN) return 0;
+size_t fastqr_ormqr_workspace_bytes(int64_t batch, int64_t m, int64_t r, int64_t k) {
+  if (batch <= 0 || r <= 0 || k <= 0 || m < r || m > kMaxN || k > 2147483647LL) return 0;
   const int64_t chunk = batch < fastqr::kMaxGridY ? batch : fastqr::kMaxGridY;
-  return (fastqr::ormqr_workspace_floats(chunk, (int)r) * sizeof(float) + 255) & ~(size_t)255;
+  return (fastqr::ormqr_workspace_floats(chunk, (int)m, (int)r, (int)k) * sizeof(float) + 255) & ~(size_t)255;
 }
 
 int fastqr_ormqr_f32(const float* H, int64_t batch, int64_t m, int64_t r, int64_t h_s0, int64_t h_s1, int64_t h_s2,
@@ -719,7 +719,7 @@ int fastqr_ormqr_f32(const float* H, int64_t batch, int64_t m, int64_t r, int64_
   if (batch > 1 && c_s0 < c_s2 * k)
     return fail(FASTQR_ELAYOUT, "C batch stride %lld smaller than one matrix (%lld)", (long long)c_s0,
                 (long long)(c_s2 * k));
-  const size_t need = fastqr_ormqr_workspace_bytes(batch, r);
+  const size_t need = fastqr_ormqr_workspace_bytes(batch, m, r, k);
   if (workspace_bytes < need || (need > 0 && workspace == nullptr))
     return fail(FASTQR_EWORKSPACE, "workspace of %zu bytes required, %zu given", need, workspace_bytes);
   if (((uintptr_t)workspace & 15) != 0) return fail(FASTQR_EWORKSPACE, "workspace must be 16-byte aligned");

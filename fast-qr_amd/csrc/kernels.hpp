@@ -81,6 +81,13 @@ struct WyrCall {
   int rows_per_blk;     // multiple of 32
   bool vec;
   bool hi_prio;         // critical path: the waves win issue arbitration on shared SIMDs
+  // ormqr: the updated columns [c_begin, c_end) are columns of a matrix X of
+  // their own (xcols columns, leading dimension ldx, n rows); V is then read
+  // from H's first vcols columns.  Not with gram.
+  float* X = nullptr;
+  int64_t xs0 = 0;
+  int ldx = 0, xcols = 0, vcols = 0;
+  bool t_trans = false;  // apply X - V T V^T X (T of the slot / Tg read transposed)
 };
 hipError_t launch_wyr(const WyrCall& c, hipStream_t stream);
 int wyr_rows_per_block(int m, int64_t batch, int cols);
@@ -109,8 +116,9 @@ hipError_t launch_orgqr(const float* H, int64_t batch, int n, int64_t hs0, int64
 // Q C or Q^T C in place in C (qr_orgqr.hip), Q = H_0 ... H_{r-1} from r
 // reflectors of m rows (H columns contiguous), C m x k (columns contiguous):
 // T of every 32-column panel, then the panels' transforms applied to C in
-// groups of kMaxWY (first to last for Q^T C, last to first for Q C).
-size_t ormqr_workspace_floats(int64_t batch, int r);
+// groups of kMaxWY (first to last for Q^T C, last to first for Q C); groups
+// taller than a strip fits run on the row-split kernels.
+size_t ormqr_workspace_floats(int64_t batch, int m, int r, int k);
 hipError_t launch_ormqr(const float* H, int64_t batch, int m, int r, int64_t hs0, int64_t ldh, const float* tau,
                         int64_t ts0, int64_t ts1, float* C, int64_t cs0, int64_t ldc, int k, bool transpose, float* ws,
                         bool vec, hipStream_t stream);

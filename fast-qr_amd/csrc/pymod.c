@@ -86,12 +86,12 @@ static PyObject* py_ormqr(PyObject* self, PyObject* const* args, Py_ssize_t narg
 
 static PyObject* py_ormqr_workspace_bytes(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
   (void)self;
-  int64_t b, r;
-  if (nargs != 2 || as_i64(args[0], &b) || as_i64(args[1], &r)) {
-    if (!PyErr_Occurred()) PyErr_SetString(PyExc_TypeError, "ormqr_workspace_bytes(batch, r)");
+  int64_t b, m, r, k;
+  if (nargs != 4 || as_i64(args[0], &b) || as_i64(args[1], &m) || as_i64(args[2], &r) || as_i64(args[3], &k)) {
+    if (!PyErr_Occurred()) PyErr_SetString(PyExc_TypeError, "ormqr_workspace_bytes(batch, m, r, k)");
     return NULL;
   }
-  return PyLong_FromSize_t(fastqr_ormqr_workspace_bytes(b, r));
+  return PyLong_FromSize_t(fastqr_ormqr_workspace_bytes(b, m, r, k));
 }
 
 static PyObject* py_orgqr_workspace_bytes(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {

@@ -46,8 +46,8 @@ __global__ void __launch_bounds__(256) orgqr_init_kernel(const float* __restrict
 __global__ void __launch_bounds__(256) orgqr_larft_kernel(const float* __restrict__ Q, int64_t qs0, int ldq, int n,
                                                           int nrefl, const float* __restrict__ tau, int64_t ts0,
                                                           int64_t ts1, int64_t batch, float* __restrict__ Tws,
-                                                          float* __restrict__ Yws, int t_trans) {
-  const int p = blockIdx.x;
+                                                          float* __restrict__ Yws, int t_trans, int p_off) {
+  const int p = p_off + blockIdx.x;
   const int64_t b = blockIdx.y;
   const int k0 = 32 * p;
   const int nb = min(32, nrefl - k0);
@@ -284,7 +284,7 @@ hipError_t launch_orgqr(const float* H, int64_t batch, int n, int64_t hs0, int64
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
   hipLaunchKernelGGL(orgqr_larft_kernel, dim3((unsigned)npan, (unsigned)batch), dim3(256), 0, stream, Q, qs0,
-                     (int)ldq, n, n, tau, ts0, ts1, batch, Tws, Yws, 1);
+                     (int)ldq, n, n, tau, ts0, ts1, batch, Tws, Yws, 1, 0);
   if ((e = hipGetLastError()) != hipSuccess) return e;
 
   auto panel_q = [&](int p) -> hipError_t {
@@ -397,37 +397,125 @@ hipError_t launch_orgqr(const float* H, int64_t batch, int n, int64_t hs0, int64
   return hipSuccess;
 }
 
-size_t ormqr_workspace_floats(int64_t batch, int r) {
+// Rows a strip-resident update holds in registers (8 waves x 8 tiles of 32);
+// taller groups of reflectors go to the row-split kernels with a group T.
+constexpr int kOrmqrResidentRows = 2048;
+// C columns per row-split call (bounds its partial-product scratch)
+constexpr int kOrmqrChunkCols = 4096;
+
+// Panel groups (kMaxWY panels each) before the first whose rows fit a strip.
+static int ormqr_tall_groups(int m, int r) {
+  const int npan = (r + 31) / 32;
+  const int ngroups = (npan + kMaxWY - 1) / kMaxWY;
+  int g = 0;
+  while (g < ngroups && m - 32 * kMaxWY * g > kOrmqrResidentRows) ++g;
+  return g;
+}
+
+size_t ormqr_workspace_floats(int64_t batch, int m, int r, int k) {
   const int64_t npan = (r + 31) / 32;
   const int64_t nchunk = (npan + kMaxSlots - 1) / kMaxSlots;
-  return (size_t)(nchunk * batch * kMaxSlots * 1024);
+  size_t f = (size_t)(nchunk * batch * kMaxSlots * 1024);
+  if (ormqr_tall_groups(m, r) > 0) {
+    const int cols = k < kOrmqrChunkCols ? k : kOrmqrChunkCols;
+    f += (size_t)batch * kWyrTgStride + wyr_workspace_floats(batch, m > cols ? m : cols);
+  }
+  return f;
 }
 
 // LAPACK sormqr (SIDE = 'L') in compact-WY form, as the blocked geqrf applies
-// a panel group: T of every 32-column panel in one orgqr_larft_kernel launch
-// (stored as T for Q^T C, whose blocks B_p^T = I - V T^T V^T are what the
-// update kernels apply with a stored T, and as T^T for Q C, whose blocks are
+// a panel group: T of every 32-column panel by orgqr_larft_kernel (stored as
+// T for Q^T C, whose blocks B_p^T = I - V T^T V^T are what the update kernels
+// apply with a stored T, and as T^T for Q C, whose blocks are
 // B_p = I - V T V^T), then one strip-resident update of every column of C per
-// group of kMaxWY panels: C is loaded and stored once per group.
+// group of kMaxWY panels: C is loaded and stored once per group.  Groups of
+// more than kOrmqrResidentRows rows are applied by the row-split kernels with
+// the group's T (its Gram matrix and panel T's joined, as geqrf's tall
+// path), read transposed for Q C; their panels' T stay untransposed for the join.
 hipError_t launch_ormqr(const float* H, int64_t batch, int m, int r, int64_t hs0, int64_t ldh, const float* tau,
                         int64_t ts0, int64_t ts1, float* C, int64_t cs0, int64_t ldc, int k, bool transpose, float* ws,
                         bool vec, hipStream_t stream) {
   if (r <= 0 || k <= 0) return hipSuccess;
   const int npan = (r + 31) / 32;
-  hipLaunchKernelGGL(orgqr_larft_kernel, dim3((unsigned)npan, (unsigned)batch), dim3(256), 0, stream, H, hs0, (int)ldh,
-                     m, r, tau, ts0, ts1, batch, ws, nullptr, transpose ? 0 : 1);
-  hipError_t e = hipGetLastError();
-  if (e != hipSuccess) return e;
-  static_assert(kMaxSlots % kMaxWY == 0, "a panel group must not straddle two T chunks");
   const int ngroups = (npan + kMaxWY - 1) / kMaxWY;
+  const int g_tall = ormqr_tall_groups(m, r);
+  const int p_tall = g_tall * kMaxWY < npan ? g_tall * kMaxWY : npan;
+  hipError_t e = hipSuccess;
+  if (p_tall > 0) {
+    hipLaunchKernelGGL(orgqr_larft_kernel, dim3((unsigned)p_tall, (unsigned)batch), dim3(256), 0, stream, H, hs0,
+                       (int)ldh, m, r, tau, ts0, ts1, batch, ws, nullptr, 0, 0);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  if (npan > p_tall) {
+    hipLaunchKernelGGL(orgqr_larft_kernel, dim3((unsigned)(npan - p_tall), (unsigned)batch), dim3(256), 0, stream, H,
+                       hs0, (int)ldh, m, r, tau, ts0, ts1, batch, ws, nullptr, transpose ? 0 : 1, p_tall);
+    if ((e = hipGetLastError()) != hipSuccess) return e;
+  }
+  const int64_t nchunk = (npan + kMaxSlots - 1) / kMaxSlots;
+  float* Tg = ws + nchunk * batch * kMaxSlots * 1024;
+  float* scratch = Tg + batch * kWyrTgStride;
+  static_assert(kMaxSlots % kMaxWY == 0, "a panel group must not straddle two T chunks");
   for (int s = 0; s < ngroups; ++s) {
     const int g = transpose ? s : ngroups - 1 - s;  // Q^T C: H_0 first; Q C: H_{r-1} first
     const int p0 = kMaxWY * g;
     const int p1 = min(p0 + kMaxWY, npan);
+    const int k0 = 32 * p0;
     const float* Tchunk = ws + (int64_t)(p0 / kMaxSlots) * batch * kMaxSlots * 1024;
-    e = launch_wy_apply(H, batch, hs0, ldh, r, C, cs0, ldc, k, Tchunk, m, 32 * p0, 32, p0 % kMaxSlots, p1 - p0, vec,
-                        stream, /*reverse=*/!transpose);
-    if (e != hipSuccess) return e;
+    if (g >= g_tall) {
+      e = launch_wy_apply(H, batch, hs0, ldh, r, C, cs0, ldc, k, Tchunk, m, k0, 32, p0 % kMaxSlots, p1 - p0, vec,
+                          stream, /*reverse=*/!transpose);
+      if (e != hipSuccess) return e;
+      continue;
+    }
+    const int kg = min(32 * (p1 - p0), r - k0);  // the group's reflectors
+    WyrCall gc{};  // group T: Gram matrix of the group's reflectors, panel T's joined
+    gc.H = const_cast<float*>(H);
+    gc.hs0 = hs0;
+    gc.ldh = (int)ldh;
+    gc.n = m;
+    gc.batch = batch;
+    gc.kv = k0;
+    gc.k = kg;
+    gc.c_begin = k0;
+    gc.c_end = k0 + kg;
+    gc.gram = true;
+    gc.use_tg = true;
+    gc.q = p1 - p0;
+    gc.nb = 32;
+    gc.slot0 = p0 % kMaxSlots;
+    gc.Tws = Tchunk;
+    gc.Tg = Tg;
+    gc.scratch = scratch;
+    gc.rows_per_blk = wyr_rows_per_block(m - k0, batch, kg);
+    gc.vec = vec;
+    gc.vcols = r;
+    if ((e = launch_wyr(gc, stream)) != hipSuccess) return e;
+    for (int c0 = 0; c0 < k; c0 += kOrmqrChunkCols) {
+      const int c1 = (k - c0 < kOrmqrChunkCols) ? k : c0 + kOrmqrChunkCols;
+      WyrCall ac{};
+      ac.H = const_cast<float*>(H);
+      ac.hs0 = hs0;
+      ac.ldh = (int)ldh;
+      ac.n = m;
+      ac.batch = batch;
+      ac.kv = k0;
+      ac.k = kg;
+      ac.c_begin = c0;
+      ac.c_end = c1;
+      ac.use_tg = true;
+      ac.Tg = Tg;
+      ac.Tws = Tchunk;
+      ac.scratch = scratch;
+      ac.rows_per_blk = wyr_rows_per_block(m - k0, batch, c1 - c0);
+      ac.vec = vec;
+      ac.X = C;
+      ac.xs0 = cs0;
+      ac.ldx = (int)ldc;
+      ac.xcols = k;
+      ac.vcols = r;
+      ac.t_trans = !transpose;
+      if ((e = launch_wyr(ac, stream)) != hipSuccess) return e;
+    }
   }
   return hipSuccess;
 }

@@ -60,24 +60,29 @@ __device__ __forceinline__ int64_t pp_index(int64_t b, int s, int rb, int blk, i
 // Tiles of a row block are software-pipelined: the X and V loads of tile t+1
 // are issued before the MFMAs of tile t (loads past the block read zeros
 // through the buffer range check).
-template <int NBLK, bool VEC>
+//
+// SEPX: the updated columns are a matrix X of their own (xcols columns,
+// leading dimension ldx, H's rows) (ormqr).  H holds vcols columns.
+template <int NBLK, bool VEC, bool SEPX>
 __global__ void __launch_bounds__(64) wyr_partial_kernel(const float* __restrict__ H, int64_t hs0, int ldh, int n,
                                                          int kv, int k, int c_begin, int c_end, int gram_end,
                                                          int rows_per_blk, float* __restrict__ Ppart, int nstrips,
-                                                         int nrb, int hi) {
+                                                         int nrb, int hi, const float* __restrict__ X_, int64_t xs0,
+                                                         int ldx, int xcols, int vcols) {
   if (hi) __builtin_amdgcn_s_setprio(2);
   const int s = blockIdx.x, rb = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int lane = threadIdx.x, h = lane >> 5, l32 = lane & 31;
   const int col = c_begin + 32 * s + l32;
   const bool colok = col < c_end;
-  const bool is_v = c_begin + 32 * s < gram_end;  // strip of the group's own columns: read as V
-  const MatBuf M{make_rsrc(H + b * hs0, (uint32_t)(4 * ldh * n)), ldh, n};
+  const bool is_v = !SEPX && c_begin + 32 * s < gram_end;  // strip of the group's own columns: read as V
+  const MatBuf M{make_rsrc(H + b * hs0, (uint32_t)(4 * ldh * vcols)), ldh, n};
+  const MatBuf Mx = SEPX ? MatBuf{make_rsrc(X_ + b * xs0, (uint32_t)(4 * ldx * xcols)), ldx, n} : M;
   const int r_lo = kv + rb * rows_per_blk;
   const int r_hi = min(n, r_lo + rows_per_blk);
 
   auto load_x = [&](int r0) -> f32x16 {
-    f32x16 x = tile_load<VEC>(M, r0, col, colok && r0 < r_hi, h);
+    f32x16 x = tile_load<VEC>(Mx, r0, col, colok && r0 < r_hi, h);
     if (is_v) {
 #pragma unroll
       for (int j = 0; j < 16; ++j) {
@@ -261,7 +266,8 @@ template <int NBLK>
 __global__ void __launch_bounds__(kSumWaves * 64) wyr_w_kernel(const float* __restrict__ Ppart, int nstrips, int nrb,
                                                                int s0, const float* __restrict__ Tsrc,
                                                                int64_t t_stride, int ldt, int k,
-                                                               float* __restrict__ Wbuf, int nstrips_w, int hi) {
+                                                               float* __restrict__ Wbuf, int nstrips_w, int hi,
+                                                               int t_trans) {
   if (hi) __builtin_amdgcn_s_setprio(2);
   const int s = blockIdx.x;
   const int64_t b = blockIdx.y;
@@ -283,14 +289,16 @@ __global__ void __launch_bounds__(kSumWaves * 64) wyr_w_kernel(const float* __re
   for (int j = 0; j < 16; ++j) W[j] = 0.0f;
 #pragma unroll
   for (int bp = 0; bp < NBLK; ++bp) {
-    if (bp > blk) break;
+    // T upper triangular: block (bp, blk) of T (of T^T with t_trans) is zero for bp > blk (bp < blk)
+    if (t_trans ? bp < blk : bp > blk) continue;
     float t[16];
     f32x16 P;
 #pragma unroll
     for (int j = 0; j < 16; ++j) {
       const int kk = 32 * bp + acc_row(j, h);
       const int cc = 32 * blk + l32;
-      t[j] = (kk < k && cc < k) ? Tb[kk * ldt + cc] : 0.0f;
+      // t_trans: W = -T P (T stored, read as T^T)
+      t[j] = (kk < k && cc < k) ? Tb[t_trans ? cc * ldt + kk : kk * ldt + cc] : 0.0f;
       P[j] = (red[0][bp][j][lane] + red[1][bp][j][lane]) + (red[2][bp][j][lane] + red[3][bp][j][lane]);
     }
 #pragma unroll
@@ -349,19 +357,22 @@ __device__ __forceinline__ void wave_form_w(f32x16 (&W)[NBLK], const float* __re
 // FW: W formed in the kernel from the partials (Ppart, strips s0 + s) and T
 // instead of read from Wbuf; every row block's wave repeats it, which costs
 // less than the separate W launch on the critical path.
-template <int NBLK, bool VEC, bool FW>
+template <int NBLK, bool VEC, bool FW, bool SEPX>
 __global__ void __launch_bounds__(64) wyr_apply_kernel(float* __restrict__ H, int64_t hs0, int ldh, int n, int kv,
                                                        int k, int c_begin, int c_end, int rows_per_blk,
                                                        const float* __restrict__ Wbuf, int nstrips_w, int hi,
                                                        const float* __restrict__ Ppart, int nstrips, int nrb, int s0,
-                                                       const float* __restrict__ Tsrc, int64_t t_stride, int ldt) {
+                                                       const float* __restrict__ Tsrc, int64_t t_stride, int ldt,
+                                                       float* __restrict__ X_, int64_t xs0, int ldx, int xcols,
+                                                       int vcols) {
   if (hi) __builtin_amdgcn_s_setprio(2);
   const int s = blockIdx.x, rb = blockIdx.y;
   const int64_t b = blockIdx.z;
   const int lane = threadIdx.x, h = lane >> 5, l32 = lane & 31;
   const int col = c_begin + 32 * s + l32;
   const bool colok = col < c_end;
-  const MatBuf M{make_rsrc(H + b * hs0, (uint32_t)(4 * ldh * n)), ldh, n};
+  const MatBuf M{make_rsrc(H + b * hs0, (uint32_t)(4 * ldh * vcols)), ldh, n};
+  const MatBuf Mx = SEPX ? MatBuf{make_rsrc(X_ + b * xs0, (uint32_t)(4 * ldx * xcols)), ldx, n} : M;
   const int r_lo = kv + rb * rows_per_blk;
   const int r_hi = min(n, r_lo + rows_per_blk);
   f32x16 W[NBLK];
@@ -380,17 +391,17 @@ __global__ void __launch_bounds__(64) wyr_apply_kernel(float* __restrict__ H, in
       v[blk] = wy_load_vb(M, kw, min(32, k - 32 * blk), r0, h, l32, r0 < r_hi && r0 + 32 > kw);
     }
   };
-  f32x16 X = tile_load<VEC>(M, r_lo, col, colok, h);
+  f32x16 X = tile_load<VEC>(Mx, r_lo, col, colok, h);
   f32x16 V[NBLK];
   load_v(r_lo, V);
   for (int r0 = r_lo; r0 < r_hi; r0 += 32) {
-    const f32x16 Xn = tile_load<VEC>(M, r0 + 32, col, colok && r0 + 32 < r_hi, h);
+    const f32x16 Xn = tile_load<VEC>(Mx, r0 + 32, col, colok && r0 + 32 < r_hi, h);
     f32x16 Vn[NBLK];
     load_v(r0 + 32, Vn);
 #pragma unroll
     for (int blk = 0; blk < NBLK; ++blk)
       if (r0 + 32 > kv + 32 * blk) wy_mfma_apply(X, V[blk], W[blk]);
-    tile_store<VEC>(M, r0, col, colok, h, X);
+    tile_store<VEC>(Mx, r0, col, colok, h, X);
     X = Xn;
 #pragma unroll
     for (int blk = 0; blk < NBLK; ++blk) V[blk] = Vn[blk];
@@ -430,14 +441,24 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
   float* Ppart = c.scratch;
   float* Wbuf = c.scratch + (size_t)c.batch * nstrips * nrb * kWyrMaxBlk * 1024;
   const dim3 gp((unsigned)nstrips, (unsigned)nrb, (unsigned)c.batch);
+  const bool sepx = c.X != nullptr;
+  const int vcols = c.vcols > 0 ? c.vcols : c.n;
+#define WYR_PARTIAL2(NB_, VEC_, SEPX_)                                                                             \
+  hipLaunchKernelGGL((wyr_partial_kernel<NB_, VEC_, SEPX_>), gp, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv, \
+                     c.k, c.c_begin, c.c_end, gram_end, c.rows_per_blk, Ppart, nstrips, nrb, hi, c.X, c.xs0, c.ldx, \
+                     c.xcols, vcols)
 #define WYR_PARTIAL(NB_)                                                                                           \
   do {                                                                                                             \
-    if (c.vec)                                                                                                     \
-      hipLaunchKernelGGL((wyr_partial_kernel<NB_, true>), gp, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv,   \
-                         c.k, c.c_begin, c.c_end, gram_end, c.rows_per_blk, Ppart, nstrips, nrb, hi);                   \
-    else                                                                                                           \
-      hipLaunchKernelGGL((wyr_partial_kernel<NB_, false>), gp, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv,  \
-                         c.k, c.c_begin, c.c_end, gram_end, c.rows_per_blk, Ppart, nstrips, nrb, hi);                   \
+    if (sepx) {                                                                                                    \
+      if (c.vec)                                                                                                   \
+        WYR_PARTIAL2(NB_, true, true);                                                                             \
+      else                                                                                                         \
+        WYR_PARTIAL2(NB_, false, true);                                                                            \
+    } else if (c.vec) {                                                                                            \
+      WYR_PARTIAL2(NB_, true, false);                                                                              \
+    } else {                                                                                                       \
+      WYR_PARTIAL2(NB_, false, false);                                                                             \
+    }                                                                                                              \
   } while (0)
   switch (nblk) {
     case 1: WYR_PARTIAL(1); break;
@@ -446,6 +467,7 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
     default: WYR_PARTIAL(4); break;
   }
 #undef WYR_PARTIAL
+#undef WYR_PARTIAL2
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
 
@@ -471,43 +493,47 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
   const int nx = nstrips - gram_strips;  // strips that are updated
   if (nx <= 0) return hipSuccess;
   // critical-path updates form W inside the apply kernel (one launch fewer)
-  const bool fw = c.hi_prio;
+  const bool fw = c.hi_prio && !sepx && !c.t_trans;
   const dim3 gw((unsigned)nx, (unsigned)c.batch);
   if (!fw) switch (nblk) {
     case 1:
       hipLaunchKernelGGL((wyr_w_kernel<1>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
-                         ldt, c.k, Wbuf, nx, hi);
+                         ldt, c.k, Wbuf, nx, hi, c.t_trans ? 1 : 0);
       break;
     case 2:
       hipLaunchKernelGGL((wyr_w_kernel<2>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
-                         ldt, c.k, Wbuf, nx, hi);
+                         ldt, c.k, Wbuf, nx, hi, c.t_trans ? 1 : 0);
       break;
     case 3:
       hipLaunchKernelGGL((wyr_w_kernel<3>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
-                         ldt, c.k, Wbuf, nx, hi);
+                         ldt, c.k, Wbuf, nx, hi, c.t_trans ? 1 : 0);
       break;
     default:
       hipLaunchKernelGGL((wyr_w_kernel<4>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
-                         ldt, c.k, Wbuf, nx, hi);
+                         ldt, c.k, Wbuf, nx, hi, c.t_trans ? 1 : 0);
       break;
   }
   if ((e = hipGetLastError()) != hipSuccess) return e;
   const int xc_begin = c.c_begin + 32 * gram_strips;
   const dim3 ga((unsigned)nx, (unsigned)nrb, (unsigned)c.batch);
-#define WYR_APPLY_FW(NB_, VEC_, FW_)                                                                               \
-  hipLaunchKernelGGL((wyr_apply_kernel<NB_, VEC_, FW_>), ga, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv, c.k, \
-                     xc_begin, c.c_end, c.rows_per_blk, Wbuf, nx, hi, Ppart, nstrips, nrb, gram_strips, Tsrc,      \
-                     t_stride, ldt)
+#define WYR_APPLY_FW(NB_, VEC_, FW_, SEPX_)                                                                        \
+  hipLaunchKernelGGL((wyr_apply_kernel<NB_, VEC_, FW_, SEPX_>), ga, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv, \
+                     c.k, xc_begin, c.c_end, c.rows_per_blk, Wbuf, nx, hi, Ppart, nstrips, nrb, gram_strips, Tsrc,   \
+                     t_stride, ldt, c.X, c.xs0, c.ldx, c.xcols, vcols)
 #define WYR_APPLY(NB_)                                                                                             \
   do {                                                                                                             \
-    if (c.vec && fw)                                                                                               \
-      WYR_APPLY_FW(NB_, true, true);                                                                               \
+    if (sepx && c.vec)                                                                                             \
+      WYR_APPLY_FW(NB_, true, false, true);                                                                        \
+    else if (sepx)                                                                                                 \
+      WYR_APPLY_FW(NB_, false, false, true);                                                                       \
+    else if (c.vec && fw)                                                                                          \
+      WYR_APPLY_FW(NB_, true, true, false);                                                                        \
     else if (c.vec)                                                                                                \
-      WYR_APPLY_FW(NB_, true, false);                                                                              \
+      WYR_APPLY_FW(NB_, true, false, false);                                                                       \
     else if (fw)                                                                                                   \
-      WYR_APPLY_FW(NB_, false, true);                                                                              \
+      WYR_APPLY_FW(NB_, false, true, false);                                                                       \
     else                                                                                                           \
-      WYR_APPLY_FW(NB_, false, false);                                                                             \
+      WYR_APPLY_FW(NB_, false, false, false);                                                                      \
   } while (0)
   switch (nblk) {
     case 1: WYR_APPLY(1); break;

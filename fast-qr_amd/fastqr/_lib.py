@@ -87,7 +87,7 @@ def cdll() -> ctypes.CDLL:
         lib.fastqr_ormqr_f32.argtypes = [vp, i64, i64, i64, i64, i64, i64, vp, i64, i64, vp, i64, i64, i64, i64,
                                          ctypes.c_int, vp, sz, vp]
         lib.fastqr_ormqr_f32.restype = ctypes.c_int
-        lib.fastqr_ormqr_workspace_bytes.argtypes = [i64, i64]
+        lib.fastqr_ormqr_workspace_bytes.argtypes = [i64, i64, i64, i64]
         lib.fastqr_ormqr_workspace_bytes.restype = sz
         lib.fastqr_workspace_bytes.restype = sz
         lib.fastqr_path_name.argtypes = [i64]

@@ -99,7 +99,7 @@ def apply_q(h: torch.Tensor, tau: torch.Tensor, c: torch.Tensor, *, transpose: b
         h = h.transpose(-1, -2).contiguous().transpose(-1, -2)
     mod = ext()
     sptr = _current_stream_ptr(idx)
-    ws = workspace.scratch(h.device, sptr, mod.ormqr_workspace_bytes(b, r))
+    ws = workspace.scratch(h.device, sptr, mod.ormqr_workspace_bytes(b, m, r, k))
     hs0, hs1, hs2 = h.stride()
     ts0, ts1 = tau.stride()
     cs0, cs1, cs2 = out.stride()

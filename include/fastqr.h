@@ -153,9 +153,10 @@ size_t fastqr_orgqr_workspace_bytes(int64_t batch, int64_t n);
  *        C[b*c_s0 + i*c_s1 + j*c_s2], columns contiguous (c_s1 == 1,
  *        c_s2 >= m); overwritten by Q C (transpose == 0) or Q^T C (!= 0).
  *        C must not overlap H or tau.
- * workspace / workspace_bytes  at least fastqr_ormqr_workspace_bytes(batch, r)
- *        bytes of device scratch, 16-byte aligned (T of every 32-column panel);
- *        may be NULL when that size is 0.
+ * workspace / workspace_bytes  at least fastqr_ormqr_workspace_bytes(batch, m,
+ *        r, k) bytes of device scratch, 16-byte aligned (T of every 32-column
+ *        panel; for m > 2048 also a group T and the row-split partial
+ *        products); may be NULL when that size is 0.
  * stream a hipStream_t; asynchronous, no host synchronisation.
  *
  * 1 <= m <= 4096.  Returns FASTQR_OK, a negative FASTQR_E* argument error, or
@@ -168,8 +169,8 @@ int fastqr_ormqr_f32(const float* H, int64_t batch, int64_t m, int64_t r,
                      int transpose, void* workspace, size_t workspace_bytes,
                      void* stream);
 
-/* Workspace bytes fastqr_ormqr_f32 needs for (batch, r). */
-size_t fastqr_ormqr_workspace_bytes(int64_t batch, int64_t r);
+/* Workspace bytes fastqr_ormqr_f32 needs for (batch, m, r, k). */
+size_t fastqr_ormqr_workspace_bytes(int64_t batch, int64_t m, int64_t r, int64_t k);
 
 /*
  * Name of the kernel path fastqr_geqrf_f32 takes for size n ("wave64",

@@ -44,7 +44,7 @@ def lib():
     lib.fastqr_ormqr_f32.argtypes = [vp, i64, i64, i64, i64, i64, i64, vp, i64, i64,
                                      vp, i64, i64, i64, i64, ctypes.c_int, vp, ctypes.c_size_t, vp]
     lib.fastqr_ormqr_f32.restype = ctypes.c_int
-    lib.fastqr_ormqr_workspace_bytes.argtypes = [i64, i64]
+    lib.fastqr_ormqr_workspace_bytes.argtypes = [i64, i64, i64, i64]
     lib.fastqr_ormqr_workspace_bytes.restype = ctypes.c_size_t
     return lib
 
@@ -76,7 +76,7 @@ def householder_product(lib, h, tau):
 
 def ormqr_(lib, h, tau, c, transpose):
     b, m, r = h.shape
-    ws_bytes = lib.fastqr_ormqr_workspace_bytes(b, r)
+    ws_bytes = lib.fastqr_ormqr_workspace_bytes(b, m, r, c.shape[2])
     ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=h.device)
     rc = lib.fastqr_ormqr_f32(h.data_ptr(), b, m, r, *h.stride(), tau.data_ptr(), *tau.stride(),
                               c.data_ptr(), c.shape[2], *c.stride(), int(transpose),

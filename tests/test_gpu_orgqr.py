@@ -126,13 +126,14 @@ def test_full_workload_q_reconstructs_input(cuda, name, idx):
 # leading column block (submissions/candidate.py:7231-7237), from CPU geqrf.
 # The shapes cover one and several panel groups, r not a multiple of 32 (a
 # partial last panel and group), k of 1 and not a multiple of 32, m not a
-# multiple of 4 (element loads), and strips taller than 2048 rows (the
-# streaming form of the update kernel).
+# multiple of 4 (element loads), and groups taller than 2048 rows (the
+# row-split kernels with a group T, also in chunks of 4096 columns of C).
 @pytest.mark.parametrize("batch,m,r,k,transpose", [
     (3, 20, 20, 5, False), (3, 100, 100, 100, True), (2, 600, 600, 7, True), (2, 600, 600, 7, False),
     (2, 512, 512, 512, False), (2, 512, 512, 512, True), (4, 300, 77, 45, False), (4, 300, 77, 45, True),
     (3, 333, 333, 1, True), (2, 333, 200, 70, False), (1, 2100, 2100, 33, True), (1, 2100, 2100, 33, False),
-    (1, 4096, 4096, 40, False)])
+    (1, 4096, 4096, 40, False), (1, 4096, 4096, 40, True), (2, 3000, 200, 50, True), (2, 3000, 200, 50, False),
+    (1, 2100, 64, 4200, True), (1, 2101, 70, 33, False)])
 def test_apply_q_matches_ormqr(cuda, batch, m, r, k, transpose):
     _say(f"[apply_q] batch={batch} m={m} r={r} k={k} transpose={transpose}")
     g = torch.Generator().manual_seed(300 + m + r)
@@ -186,7 +187,7 @@ def test_ormqr_c_abi_with_padded_c(cuda):
     c_ref = torch.ormqr(h.cpu().double(), tau.cpu().double(), cview.cpu().double(), left=True, transpose=True)
     before = cbuf.cpu()
     lib = fastqr.cdll()
-    nbytes = lib.fastqr_ormqr_workspace_bytes(b, m)
+    nbytes = lib.fastqr_ormqr_workspace_bytes(b, m, m, k)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=cuda)
     torch.cuda.synchronize()
     rc = lib.fastqr_ormqr_f32(h.data_ptr(), b, m, m, *h.stride(), tau.data_ptr(), *tau.stride(), cview.data_ptr(), k,

@@ -57,7 +57,8 @@ def test_workspace_bytes():
     assert lib.fastqr_workspace_bytes(0, 512) == 0
     small = lib.fastqr_workspace_bytes(1, 512)
     assert small > 0 and small % 256 == 0
-    assert lib.fastqr_workspace_bytes(640, 512) >= 640 * small - 255
+    # the T slots (12 of 32 x 32 floats per matrix) scale with the batch
+    assert lib.fastqr_workspace_bytes(640, 512) >= 640 * 12 * 32 * 32 * 4
 
 
 def _call(lib, A=8, b=2, n=100, a_s=(None,), H=16, h_s=None, tau=32, t_s=None, ws=64, ws_bytes=1 << 20):
@@ -277,11 +278,17 @@ def _ormqr_call(lib, H=8, b=2, m=100, r=100, h_s=None, tau=32, t_s=None, C=16, k
 
 def test_ormqr_argument_validation_returns_codes_without_launching():
     lib = fastqr.cdll()
-    assert lib.fastqr_ormqr_workspace_bytes(0, 64) == 0
-    assert lib.fastqr_ormqr_workspace_bytes(2, 0) == 0
-    one = lib.fastqr_ormqr_workspace_bytes(1, 512)
+    assert lib.fastqr_ormqr_workspace_bytes(0, 64, 64, 8) == 0
+    assert lib.fastqr_ormqr_workspace_bytes(2, 64, 0, 8) == 0
+    assert lib.fastqr_ormqr_workspace_bytes(2, 64, 64, 0) == 0
+    assert lib.fastqr_ormqr_workspace_bytes(2, 64, 65, 8) == 0  # r > m: rejected by the call itself
+    one = lib.fastqr_ormqr_workspace_bytes(1, 512, 512, 100)
     assert one >= 16 * 32 * 32 * 4 and one % 256 == 0  # a T factor per 32-column panel
-    assert lib.fastqr_ormqr_workspace_bytes(640, 512) >= 640 * one - 255
+    assert lib.fastqr_ormqr_workspace_bytes(640, 512, 512, 100) >= 640 * one - 255
+    # above 2048 rows also a group T and the row-split partial products, bounded in k
+    tall = lib.fastqr_ormqr_workspace_bytes(2, 4096, 4096, 4096)
+    assert tall > lib.fastqr_ormqr_workspace_bytes(2, 2048, 2048, 4096) > 0
+    assert lib.fastqr_ormqr_workspace_bytes(2, 4096, 4096, 100000) == tall
     # nothing to do: empty batch, no rows, no columns of C, no reflectors (Q = I)
     for kw in ({"b": 0}, {"m": 0, "r": 0}, {"k": 0}, {"r": 0}):
         assert _ormqr_call(lib, **kw) == _lib.FASTQR_OK
