@@ -358,10 +358,10 @@ int geqrf_impl(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a
   hipError_t e = hipSuccess;
   const double bd = (double)batch;
   // A -> H, columns [c0, c1)
-  auto copy_cols = [&](int c0, int c1) -> hipError_t {
+  auto copy_cols = [&](int c0, int c1, int max_wgs = 0) -> hipError_t {
     if (same || c1 <= c0) return hipSuccess;
     return timed(kCopy, 0.0, bd * 8.0 * (double)n * (double)(c1 - c0), stream, [&] {
-      return fastqr::launch_copy_colmajor(A, batch, ni, a_s0, a_s1, a_s2, H, h_s0, h_s2, c0, c1, stream);
+      return fastqr::launch_copy_colmajor(A, batch, ni, a_s0, a_s1, a_s2, H, h_s0, h_s2, c0, c1, stream, max_wgs);
     });
   };
   if (use_rowsplit(batch, n)) {
@@ -473,21 +473,28 @@ int geqrf_impl(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a
   int rest_cus = 0;
   if (num_cus > 0 && batch < num_cus / 2)
     rest_cus = (4 * batch <= num_cus / 2) ? num_cus - 4 * (int)batch : num_cus - (int)batch;
-  auto run_update = [&](const Group& G, int c_begin, int c_end, bool critical, hipStream_t st) -> hipError_t {
+  // from_a: the columns are read from the row-major input A (their first update; not copied)
+  auto run_update = [&](const Group& G, int c_begin, int c_end, bool critical, hipStream_t st,
+                        bool from_a = false) -> hipError_t {
     if (c_end <= c_begin) return hipSuccess;
     const double m = ni - G.g0, wg = G.g_end - G.g0, c = c_end - c_begin;
     return timed(kUpdate, bd * 4.0 * m * wg * c, bd * (8.0 * m * c + 4.0 * m * wg), st, [&] {
       return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, G.g0, kTw, G.slot_base,
                                       (G.g_end - G.g0 + kTw - 1) / kTw, c_begin, c_end, vec, critical,
-                                      critical ? 0 : rest_cus, st);
+                                      critical ? 0 : rest_cus, st, false, from_a ? A : nullptr, a_s0, a_s1);
     });
   };
 
   // With the side stream, only the first group's columns are copied before
-  // its panels start; the rest of the copy (HBM-bound) runs on the caller's
-  // stream beside those panels (latency-bound) and ahead of the first
-  // look-ahead update, the first kernel that reads those columns.
+  // its panels start.  A row-major input is not copied any further: the first
+  // group's look-ahead and wide updates, the first kernels that touch the
+  // other columns, read them from A and write them to H (one read of A and no
+  // extra pass over H; a copy beside the first group's panels takes HBM and
+  // CU slots from them).  Other layouts copy the rest on the caller's stream
+  // beside those panels, ahead of the first look-ahead update.
   const int c_first = aux ? groups[0].g_end : ni;
+  const bool from_a = aux && !same && a_s2 == 1 && a_s1 >= n &&
+                      4 * ((n - 1) * a_s1 + n) < ((int64_t)1 << 31);
   if ((e = copy_cols(0, c_first)) != hipSuccess) return hip_fail(e, "copy launch");
   if (!aux) {
     for (int g = 0; g < ngroups; ++g) {
@@ -516,16 +523,22 @@ int geqrf_impl(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a
   if (!ev) return fail(FASTQR_EINVAL, "cannot record HIP events");
   if ((e = hipStreamWaitEvent(side, ev, 0)) != hipSuccess) return hip_fail(e, "stream join");
   if ((e = run_panels(groups[0], side)) != hipSuccess) return hip_fail(e, "panel launch");
-  if ((e = copy_cols(c_first, ni)) != hipSuccess) return hip_fail(e, "copy launch");
+  // Four workgroups per CU keep the copy at HBM speed and leave the CUs' other
+  // slots to the first group's panels: uncapped, its tens of thousands of
+  // small workgroups fill every CU and the panels wait for the copy to drain
+  // (640 x 512: the first panel 46 -> 196 us beside it).
+  if (!from_a && (e = copy_cols(c_first, ni, num_cus > 0 ? 4 * num_cus : 0)) != hipSuccess)
+    return hip_fail(e, "copy launch");
   // columns of the next look-ahead update ready (first: the copy)
-  hipEvent_t ev_near = c_first < ni ? record(stream) : nullptr;
-  if (c_first < ni && !ev_near) return fail(FASTQR_EINVAL, "cannot record HIP events");
+  hipEvent_t ev_near = (c_first < ni && !from_a) ? record(stream) : nullptr;
+  if (c_first < ni && !from_a && !ev_near) return fail(FASTQR_EINVAL, "cannot record HIP events");
   hipEvent_t ev_rest[kMaxGroups] = {};  // group g's wide update ended
   for (int g = 0; g + 1 < ngroups; ++g) {
     const Group& G = groups[g];
     const Group& Nx = groups[g + 1];
     if (ev_near && (e = hipStreamWaitEvent(side, ev_near, 0)) != hipSuccess) return hip_fail(e, "stream join");
-    if ((e = run_update(G, Nx.g0, Nx.g_end, true, side)) != hipSuccess) return hip_fail(e, "update launch");
+    if ((e = run_update(G, Nx.g0, Nx.g_end, true, side, from_a && g == 0)) != hipSuccess)
+      return hip_fail(e, "update launch");
     hipEvent_t ev_la = record(side);
     if (!ev_la) return fail(FASTQR_EINVAL, "cannot record HIP events");
     if (g >= 2 && (e = hipStreamWaitEvent(side, ev_rest[g - 2], 0)) != hipSuccess) return hip_fail(e, "stream join");
@@ -534,9 +547,11 @@ int geqrf_impl(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a
     ev_near = nullptr;
     if (g + 2 < ngroups) {
       const Group& N2 = groups[g + 2];
-      if ((e = run_update(G, N2.g0, N2.g_end, false, stream)) != hipSuccess) return hip_fail(e, "update launch");
+      if ((e = run_update(G, N2.g0, N2.g_end, false, stream, from_a && g == 0)) != hipSuccess)
+        return hip_fail(e, "update launch");
       if (!(ev_near = record(stream))) return fail(FASTQR_EINVAL, "cannot record HIP events");
-      if ((e = run_update(G, N2.g_end, ni, false, stream)) != hipSuccess) return hip_fail(e, "update launch");
+      if ((e = run_update(G, N2.g_end, ni, false, stream, from_a && g == 0)) != hipSuccess)
+        return hip_fail(e, "update launch");
     }
     if (!(ev_rest[g] = record(stream))) return fail(FASTQR_EINVAL, "cannot record HIP events");
   }

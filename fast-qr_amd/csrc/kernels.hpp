@@ -23,9 +23,11 @@ constexpr int64_t kMaxGridY = 65535;
 
 // Blocked path (qr_blocked.hip).
 // Copy columns [c0, c1) of A (any strides) into H (columns contiguous); c0 a
-// multiple of 64.
+// multiple of 64.  max_wgs > 0 caps the grid (the workgroups loop over the
+// 64 x 64 tiles).
 hipError_t launch_copy_colmajor(const float* A, int64_t batch, int n, int64_t as0, int64_t as1, int64_t as2,
-                                float* H, int64_t hs0, int64_t ldh, int c0, int c1, hipStream_t stream);
+                                float* H, int64_t hs0, int64_t ldh, int c0, int c1, hipStream_t stream,
+                                int max_wgs = 0);
 // Panel width (32, or 16 above 2048 rows) and the tallest panel supported (qr_panel.hip).
 int panel_width_for(int m);
 // Panel width of the strip-resident path (64 or 32; T slots of 32 columns).
@@ -46,9 +48,14 @@ hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float
 // `reverse`).  max_cus > 0 caps the grid at that many CUs' worth of resident
 // workgroups (the workgroups then loop over the work), leaving the other CUs
 // to kernels on another stream.
+// With A (row-major, leading dimension lda, batch stride as0) the columns
+// [c_begin, c_end) are read from A instead of H and written to H (their first
+// update, when the blocked path did not copy them); strips of at most 2048
+// rows.
 hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n,
                             int k0, int nb, int slot0, int nwy, int c_begin, int c_end, bool vec, bool hi_prio,
-                            int max_cus, hipStream_t stream, bool reverse = false);
+                            int max_cus, hipStream_t stream, bool reverse = false, const float* A = nullptr,
+                            int64_t as0 = 0, int64_t lda = 0);
 // The same transforms applied to a matrix C of its own (ormqr): V from the
 // first vcols columns of the factors (leading dimension ldv, m rows), C with
 // ccols columns (leading dimension ldc, m rows), every column of C updated.

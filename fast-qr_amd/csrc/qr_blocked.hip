@@ -25,14 +25,10 @@ namespace fastqr {
 // Copy modes: element loads (any strides), 16-byte row segments transposed
 // through LDS (row-major source), 16-byte column segments (column-major).
 constexpr int kCopyScalar = 0, kCopyRowVec = 1, kCopyColVec = 2;
-__global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __restrict__ A, int64_t as0,
-                                                                int64_t as1, int64_t as2,
-                                                                float* __restrict__ H, int64_t hs0,
-                                                                int64_t ldh, int n, int ntile, int tj0, int mode) {
-  __shared__ float tile[64][65];
-  const int64_t b = blockIdx.y;
-  const int ti = blockIdx.x % ntile;
-  const int tj = tj0 + (int)(blockIdx.x / ntile);
+// One 64 x 64 tile (row block ti, column block tj) of matrix b.
+__device__ __forceinline__ void copy_tile(const float* __restrict__ A, int64_t as0, int64_t as1, int64_t as2,
+                                          float* __restrict__ H, int64_t hs0, int64_t ldh, int n, int mode,
+                                          int64_t b, int ti, int tj, float (*tile)[65]) {
   const float* Ab = A + b * as0;
   float* Hb = H + b * hs0;
   const int tid = threadIdx.x;
@@ -107,6 +103,25 @@ __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __re
   }
 }
 
+// Tiles (matrix, row block, column block from tj0) in order, workgroup L
+// taking tiles L, L + gridDim.x, ...: a grid smaller than the tile count
+// leaves the CUs' other slots to kernels on another stream (an HBM-bound copy
+// does not need them all).
+__global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __restrict__ A, int64_t as0,
+                                                                int64_t as1, int64_t as2,
+                                                                float* __restrict__ H, int64_t hs0,
+                                                                int64_t ldh, int n, int ntile, int ntj, int tj0,
+                                                                int mode, int64_t total) {
+  __shared__ float tile[64][65];
+  const int per_matrix = ntile * ntj;
+  for (int64_t L = blockIdx.x; L < total; L += gridDim.x) {
+    const int64_t b = L / per_matrix;
+    const int t = (int)(L - b * per_matrix);
+    copy_tile(A, as0, as1, as2, H, hs0, ldh, n, mode, b, t % ntile, tj0 + t / ntile, tile);
+    __syncthreads();  // the next tile rewrites `tile`
+  }
+}
+
 // ---------------------------------------------------------------------------
 // Trailing update  A2 <- A2 - V T^T V^T A2  (fp32 MFMA 32x32x2)
 // ---------------------------------------------------------------------------
@@ -125,11 +140,18 @@ __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __re
 // SEPX: the updated columns live in a matrix X of their own (xcols columns,
 // leading dimension ldx, rows as H's) instead of H, and V is read from H's
 // first vcols columns (ormqr: Q C or Q^T C with V, T from a factorisation).
-template <int NW, int TPW, bool RES, bool VEC, bool SEPX>
+//
+// LOADA (strip-resident only): the strip's tiles are first read from the
+// row-major input A (leading dimension lda, a_bytes per matrix) instead of H
+// -- the first update of columns the blocked path did not copy -- and stored
+// to H as usual.
+template <int NW, int TPW, bool RES, bool VEC, bool SEPX, bool LOADA>
 __device__ __forceinline__ void wy_update_item(float* __restrict__ H, int64_t hs0, int64_t ldh, int vcols,
                                                float* __restrict__ X_, int64_t xs0, int64_t ldx, int xcols,
                                                const float* __restrict__ Tws, int n, int k0, int nb, int slot0,
-                                               int nwy, int rev, int c_begin, int c_end, int64_t b, int strip) {
+                                               int nwy, int rev, int c_begin, int c_end, int64_t b, int strip,
+                                               const float* __restrict__ A, int64_t as0, int lda, uint32_t a_bytes) {
+  static_assert(!LOADA || (RES && !SEPX), "A is read by the strip-resident geqrf update only");
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // uniform: scalar branches on tiles
   const int h = lane >> 5;
@@ -159,7 +181,14 @@ __device__ __forceinline__ void wy_update_item(float* __restrict__ H, int64_t hs
   // flight before their LDS writes: the latencies overlap instead of one
   // global load per LDS write in turn.
   f32x16 X[TPW];
-  if constexpr (RES) {
+  if constexpr (LOADA) {
+    const rsrc_t ra = make_rsrc(A + b * as0, a_bytes);
+#pragma unroll
+    for (int t = 0; t < TPW; ++t) {
+      const int rt = wave + NW * t;
+      X[t] = tile_load_rm(ra, lda, n, k0 + 32 * rt, col, colok && rt < ntiles, h);
+    }
+  } else if constexpr (RES) {
 #pragma unroll
     for (int t = 0; t < TPW; ++t) {
       const int rt = wave + NW * t;
@@ -315,12 +344,13 @@ __device__ __forceinline__ void wy_update_item(float* __restrict__ H, int64_t hs
 // than the item count loops (stride a multiple of 8, so each workgroup stays
 // on its XCD's matrices): the caller uses it to leave CUs free for the
 // critical-path kernels on the other stream.
-template <int NW, int TPW, bool RES, bool VEC, bool SEPX>
+template <int NW, int TPW, bool RES, bool VEC, bool SEPX, bool LOADA>
 __global__ void __launch_bounds__(NW * 64)
 __attribute__((amdgpu_waves_per_eu((TPW >= 2 && NW >= 4) || (TPW >= 4 && NW <= 4) ? 2 : 4, 8)))
 wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, int vcols, float* __restrict__ X, int64_t xs0,
                  int64_t ldx, int xcols, const float* __restrict__ Tws, int n, int k0, int nb, int slot0, int nwy,
-                 int rev, int c_begin, int c_end, int hi_prio, int nstrips, int batch) {
+                 int rev, int c_begin, int c_end, int hi_prio, int nstrips, int batch, const float* __restrict__ A,
+                 int64_t as0, int lda, uint32_t a_bytes) {
   // updates on the critical path (the rest of a panel group, the next group's
   // columns) win issue arbitration against the wide update they overlap
   if (hi_prio) __builtin_amdgcn_s_setprio(2);
@@ -330,8 +360,8 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, int vcols, flo
     const int64_t b = (L & 7) + 8 * (xk / nstrips);
     const int strip = xk % nstrips;
     if (b < batch)
-      wy_update_item<NW, TPW, RES, VEC, SEPX>(H, hs0, ldh, vcols, X, xs0, ldx, xcols, Tws, n, k0, nb, slot0, nwy, rev,
-                                              c_begin, c_end, b, strip);
+      wy_update_item<NW, TPW, RES, VEC, SEPX, LOADA>(H, hs0, ldh, vcols, X, xs0, ldx, xcols, Tws, n, k0, nb, slot0,
+                                                     nwy, rev, c_begin, c_end, b, strip, A, as0, lda, a_bytes);
     __syncthreads();  // the next item rewrites the LDS buffers
   }
 }
@@ -340,7 +370,7 @@ wy_update_kernel(float* __restrict__ H, int64_t hs0, int64_t ldh, int vcols, flo
 // Host-side launchers
 // ---------------------------------------------------------------------------
 hipError_t launch_copy_colmajor(const float* A, int64_t batch, int n, int64_t as0, int64_t as1, int64_t as2,
-                                float* H, int64_t hs0, int64_t ldh, int c0, int c1, hipStream_t stream) {
+                                float* H, int64_t hs0, int64_t ldh, int c0, int c1, hipStream_t stream, int max_wgs) {
   if (c0 < 0 || (c0 & 63) != 0 || c1 > n) return hipErrorInvalidValue;
   if (c1 <= c0) return hipSuccess;
   const int ntile = (n + 63) / 64;
@@ -350,15 +380,12 @@ hipError_t launch_copy_colmajor(const float* A, int64_t batch, int n, int64_t as
   const int mode = (h_vec && as2 == 1 && (as1 & 3) == 0)   ? kCopyRowVec
                    : (h_vec && as1 == 1 && (as2 & 3) == 0) ? kCopyColVec
                                                            : kCopyScalar;
-  // the batch goes to grid.y: at most kMaxGridY matrices per launch
-  for (int64_t b0 = 0; b0 < batch; b0 += kMaxGridY) {
-    const int64_t nb = (batch - b0 < kMaxGridY) ? batch - b0 : kMaxGridY;
-    hipLaunchKernelGGL(copy_to_colmajor_kernel, dim3(ntile * ntj, (unsigned)nb), dim3(256), 0, stream, A + b0 * as0,
-                       as0, as1, as2, H + b0 * hs0, hs0, ldh, n, ntile, tj0, mode);
-    const hipError_t e = hipGetLastError();
-    if (e != hipSuccess) return e;
-  }
-  return hipSuccess;
+  const int64_t total = batch * ntile * ntj;
+  int64_t grid = total < ((int64_t)1 << 30) ? total : ((int64_t)1 << 30);
+  if (max_wgs > 0 && grid > max_wgs) grid = max_wgs;
+  hipLaunchKernelGGL(copy_to_colmajor_kernel, dim3((unsigned)grid), dim3(256), 0, stream, A, as0, as1, as2, H, hs0, ldh,
+                     n, ntile, ntj, tj0, mode, total);
+  return hipGetLastError();
 }
 
 namespace {
@@ -384,7 +411,7 @@ template <bool SEPX>
 static hipError_t launch_wy(float* H, int64_t batch, int64_t hs0, int64_t ldh, int vcols, float* X, int64_t xs0,
                             int64_t ldx, int xcols, const float* Tws, int n, int k0, int nb, int slot0, int nwy,
                             int c_begin, int c_end, bool vec, bool hi_prio, int max_cus, hipStream_t stream,
-                            bool reverse) {
+                            bool reverse, const float* A = nullptr, int64_t as0 = 0, int64_t lda = 0) {
   const int cols = c_end - c_begin;
   if (cols <= 0 || nwy <= 0) return hipSuccess;
   const int ntiles = (n - k0 + 31) / 32;
@@ -430,15 +457,25 @@ static hipError_t launch_wy(float* H, int64_t batch, int64_t hs0, int64_t ldh, i
   const bool res = nw * tpw >= ntiles;
   const int prio = hi_prio ? 1 : 0;
   const int rv = reverse ? 1 : 0;
+  const bool loada = !SEPX && A != nullptr;
+  if (loada && !res) return hipErrorInvalidValue;  // only the strip-resident forms read A
+  const uint32_t a_bytes = loada ? (uint32_t)(4 * ((int64_t)(n - 1) * lda + n)) : 0u;
   auto go = [&](auto kernel, int threads) -> hipError_t {
     hipLaunchKernelGGL(kernel, grid_for(kernel, threads), dim3(threads), 0, stream, H, hs0, ldh, vcols, X, xs0, ldx,
-                       xcols, Tws, n, k0, nb, slot0, nwy, rv, c_begin, c_end, prio, ns, nbatch);
+                       xcols, Tws, n, k0, nb, slot0, nwy, rv, c_begin, c_end, prio, ns, nbatch, A, as0, (int)lda,
+                       a_bytes);
     return hipGetLastError();
   };
 #define FASTQR_WY(NW, TPW, RES)                                                                     \
-  if (nw == NW && tpw == TPW && res == RES)                                                         \
-    return vec ? go(wy_update_kernel<NW, TPW, RES, true, SEPX>, NW * 64)                            \
-               : go(wy_update_kernel<NW, TPW, RES, false, SEPX>, NW * 64);
+  if (nw == NW && tpw == TPW && res == RES) {                                                       \
+    if constexpr (!SEPX) {                                                                          \
+      if (loada)                                                                                    \
+        return vec ? go(wy_update_kernel<NW, TPW, RES, true, SEPX, true>, NW * 64)                  \
+                   : go(wy_update_kernel<NW, TPW, RES, false, SEPX, true>, NW * 64);                \
+    }                                                                                               \
+    return vec ? go(wy_update_kernel<NW, TPW, RES, true, SEPX, false>, NW * 64)                     \
+               : go(wy_update_kernel<NW, TPW, RES, false, SEPX, false>, NW * 64);                   \
+  }
   FASTQR_WY(1, 1, true)
   FASTQR_WY(2, 1, true)
   FASTQR_WY(4, 1, true)
@@ -454,14 +491,15 @@ static hipError_t launch_wy(float* H, int64_t batch, int64_t hs0, int64_t ldh, i
   FASTQR_WY(8, 8, true)
 #undef FASTQR_WY
   // strips taller than 8 waves x 8 tiles: stream the tiles
-  return vec ? go(wy_update_kernel<16, 1, false, true, SEPX>, 1024) : go(wy_update_kernel<16, 1, false, false, SEPX>, 1024);
+  return vec ? go(wy_update_kernel<16, 1, false, true, SEPX, false>, 1024)
+             : go(wy_update_kernel<16, 1, false, false, SEPX, false>, 1024);
 }
 
 hipError_t launch_wy_update(float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n,
                             int k0, int nb, int slot0, int nwy, int c_begin, int c_end, bool vec, bool hi_prio,
-                            int max_cus, hipStream_t stream, bool reverse) {
+                            int max_cus, hipStream_t stream, bool reverse, const float* A, int64_t as0, int64_t lda) {
   return launch_wy<false>(H, batch, hs0, ldh, n, H, hs0, ldh, n, Tws, n, k0, nb, slot0, nwy, c_begin, c_end, vec,
-                          hi_prio, max_cus, stream, reverse);
+                          hi_prio, max_cus, stream, reverse, A, as0, lda);
 }
 
 hipError_t launch_wy_apply(const float* V, int64_t batch, int64_t vs0, int64_t ldv, int vcols, float* C, int64_t cs0,

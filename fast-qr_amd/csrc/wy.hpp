@@ -41,6 +41,22 @@ __device__ __forceinline__ f32x16 tile_load(const MatBuf& M, int r0, int col, bo
   return x;
 }
 
+// The same tile from a row-major matrix (element (row, col) at byte offset
+// 4 * (row * lda + col) of descriptor r, n rows): the 32 lanes of a half read
+// 32 consecutive columns of one row per load (128 contiguous bytes).
+__device__ __forceinline__ f32x16 tile_load_rm(rsrc_t r, int lda, int n, int r0, int col, bool ok, int h) {
+  f32x16 x;
+#pragma unroll
+  for (int q = 0; q < 4; ++q) {
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      const int row = r0 + 8 * q + 4 * h + i;
+      x[4 * q + i] = buf_load(r, (ok && row < n) ? 4u * (uint32_t)(row * lda + col) : kOffNone);
+    }
+  }
+  return x;
+}
+
 template <bool VEC>
 __device__ __forceinline__ void tile_store(const MatBuf& M, int r0, int col, bool ok, int h, const f32x16& x) {
 #pragma unroll

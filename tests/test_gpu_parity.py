@@ -162,8 +162,8 @@ def test_blocked_path_column_major_input(cuda, batch, n):
 
 @pytest.mark.parametrize("n", [352, 600])
 def test_blocked_path_generic_strides(cuda, n):
-    # a padded column-major batch (16-byte column segments), and every other
-    # row of a taller batch (element loads)
+    # a padded column-major batch (16-byte column segments), every other row
+    # of a taller batch and a row-major batch with padded rows
     _say(f"[strided blocked] n={n}")
     a = gaussian(3, n, 900 + n)
     h_rm, t_rm = run_gpu(a, cuda)
@@ -181,6 +181,17 @@ def test_blocked_path_generic_strides(cuda, n):
     h2, tau2 = custom_kernel(view2)
     torch.cuda.synchronize()
     assert torch.equal(h2.cpu(), h_rm) and torch.equal(tau2.cpu(), t_rm)
+    # row-major with a leading dimension of n + 3 (rows not 16-byte aligned):
+    # the columns right of the first panel group are read straight from A by
+    # their first update, as for the contiguous input, and the column-major
+    # view above took the copy instead -- all three bitwise equal
+    padded = torch.zeros((3, n, n + 3))
+    padded[:, :, :n] = a
+    view3 = padded.to(cuda)[:, :, :n]
+    assert view3.stride() == (n * (n + 3), n + 3, 1)
+    h3, tau3 = custom_kernel(view3)
+    torch.cuda.synchronize()
+    assert torch.equal(h3.cpu(), h_rm) and torch.equal(tau3.cpu(), t_rm)
     assert_parity(a, h_rm, t_rm)
 
 
