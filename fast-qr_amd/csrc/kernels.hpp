@@ -47,7 +47,9 @@ hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float
 // columns [c_begin, c_end), rows [k0, n), first to last (last to first with
 // `reverse`).  max_cus > 0 caps the grid at that many CUs' worth of resident
 // workgroups (the workgroups then loop over the work), leaving the other CUs
-// to kernels on another stream.
+// to kernels on another stream; kWyLeaveOneSlot caps it at one workgroup per
+// CU fewer than fit, leaving a slot on every CU.
+constexpr int kWyLeaveOneSlot = -1;
 // With A (row-major, leading dimension lda, batch stride as0) the columns
 // [c_begin, c_end) are read from A instead of H and written to H (their first
 // update, when the blocked path did not copy them); strips of at most 2048

@@ -403,6 +403,19 @@ int wgs_per_cu(K kernel, int threads) {
   return v;
 }
 
+// Compute units of the current device (queried once per device and thread).
+int device_cus() {
+  thread_local std::unordered_map<int, int> cache;
+  int dev = 0;
+  if (hipGetDevice(&dev) != hipSuccess) return 1;
+  auto it = cache.find(dev);
+  if (it != cache.end()) return it->second;
+  int v = 0;
+  if (hipDeviceGetAttribute(&v, hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess || v < 1) v = 1;
+  cache.emplace(dev, v);
+  return v;
+}
+
 }  // namespace
 
 // Shared by launch_wy_update (X = H) and launch_wy_apply (X a matrix of its
@@ -423,10 +436,14 @@ static hipError_t launch_wy(float* H, int64_t batch, int64_t hs0, int64_t ldh, i
   // grid: every item, or at most max_cus CUs' worth of resident workgroups
   auto grid_for = [&](auto kernel, int threads) -> dim3 {
     int64_t g = items;
+    int64_t cap = 0;
     if (max_cus > 0) {
-      const int64_t cap = ((int64_t)max_cus * wgs_per_cu(kernel, threads)) & ~(int64_t)7;
-      if (cap >= 8 && cap < g) g = cap;
+      cap = ((int64_t)max_cus * wgs_per_cu(kernel, threads)) & ~(int64_t)7;
+    } else if (max_cus == kWyLeaveOneSlot) {
+      const int w = wgs_per_cu(kernel, threads);
+      cap = ((int64_t)device_cus() * (w > 1 ? w - 1 : 1)) & ~(int64_t)7;
     }
+    if (cap >= 8 && cap < g) g = cap;
     return dim3((unsigned)g);
   };
   // Tiles per wave: as few as the launch's size allows, so that a strip's
