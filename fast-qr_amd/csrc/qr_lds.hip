@@ -9,12 +9,13 @@
 // multiple of 4, plus 4 so that the 32 lanes of an MFMA tile load, one column
 // each, fall in different banks) is read once from HBM, factored in LDS, and
 // written once.  Per 32-column panel:
-//   * panel_body (panel.hpp) factors the panel from LDS in registers, with
-//     wavefront DPP / permlane reductions: four waves while the panel is taller
-//     than 64 rows, one wave (no barriers) below;
-//   * the four waves apply the panel's compact-WY transform to the 32-column
-//     strips right of it with v_mfma_f32_32x32x2f32, every operand read from
-//     LDS:  X <- X - V (T^T (V^T X)).
+//   * panel_body (panel.hpp) factors the panel from LDS in registers on one
+//     wave (no barriers), with wavefront DPP / permlane reductions, while the
+//     other three waves apply the previous panel's transform to the strips
+//     right of this panel;
+//   * the panel's compact-WY transform is applied to the next strip with
+//     v_mfma_f32_32x32x2f32, every operand read from LDS,
+//     X <- X - V (T^T (V^T X)), its tiles split over three waves.
 // Rows between n and LDM stay zero throughout (the reflectors never touch
 // them), so 4-row groups need no per-row masking.
 #include "kernels.hpp"
@@ -25,6 +26,7 @@ namespace fastqr {
 namespace {
 
 constexpr int kLdsWaves = 4;
+constexpr int kCritWaves = 3;  // waves sharing the next strip's update (LDS for their partials)
 constexpr int kLdsMaxTiles = (kLdsMaxN + 31) / 32;          // 32-row MFMA tiles of a strip
 constexpr int kLdsMaxLd = ((kLdsMaxN + 3) & ~3) + 4;         // leading dimension for n = kLdsMaxN
 
@@ -182,6 +184,118 @@ __device__ __forceinline__ void lds_update(float* M, int ldm, int n, int npad, i
   }
 }
 
+// The next strip's update after a panel (the critical path), its tiles split
+// over the first kCritWaves waves (wave w takes tiles w, w + kCritWaves, ...):
+// each forms the partial P of its tiles, the partials meet in LDS (summed in
+// wave order, bitwise reproducible), every splitting wave forms W = -T^T P and
+// applies it to its own tiles.  All kLdsWaves waves pass the two barriers.
+template <int NT>
+__device__ __forceinline__ void lds_update_strip_split(float* M, int ldm, int n, int npad, int k0,
+                                                       const float (*Tk)[33], int c0, int wave, int h, int l32,
+                                                       float (*Pp)[16][64]) {
+  constexpr int TW = (NT + kCritWaves - 1) / kCritWaves;  // tiles per splitting wave, at most
+  const int col = c0 + l32;
+  const bool colok = col < n;
+  const bool active = wave < kCritWaves;
+  const int lane = 32 * h + l32;
+  f32x16 X[TW];
+  f32x16 P;
+#pragma unroll
+  for (int j = 0; j < 16; ++j) P[j] = 0.0f;
+  const float* Vc = M + (k0 + l32) * ldm;  // pattern A: this lane's reflector
+#pragma unroll
+  for (int i = 0; i < TW; ++i) {
+    const int t = wave + kCritWaves * i;
+    const bool tok = active && t < NT;
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int rb = k0 + 32 * t + 8 * q + 4 * h;
+      const f32x4 v = lds_load4(M, col * ldm + rb, tok && colok && rb < npad);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) X[i][4 * q + e] = v[e];
+    }
+#pragma unroll
+    for (int q = 0; q < 4; ++q) {
+      const int rb = k0 + 32 * t + 8 * q + 4 * h;
+      const f32x4 v = lds_load4(Vc, rb, tok && rb < npad);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int rr = 32 * t + 8 * q + 4 * h + e;  // row within the panel
+        const float vv = (rr < l32) ? 0.0f : (rr == l32 ? 1.0f : v[e]);
+        P = __builtin_amdgcn_mfma_f32_32x32x2f32(vv, X[i][4 * q + e], P, 0, 0, 0);
+      }
+    }
+  }
+  if (active) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) Pp[wave][j][lane] = P[j];
+  }
+  __syncthreads();
+  if (active) {
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      float acc = Pp[0][j][lane];
+#pragma unroll
+      for (int w = 1; w < kCritWaves; ++w) acc += Pp[w][j][lane];
+      P[j] = acc;
+    }
+    f32x16 W;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) W[j] = 0.0f;
+#pragma unroll
+    for (int j = 0; j < 16; ++j) {
+      const int kk = 8 * (j >> 2) + 4 * h + (j & 3);
+      W = __builtin_amdgcn_mfma_f32_32x32x2f32(Tk[kk][l32], P[j], W, 0, 0, 0);
+    }
+#pragma unroll
+    for (int j = 0; j < 16; ++j) W[j] = -W[j];
+#pragma unroll
+    for (int i = 0; i < TW; ++i) {
+      const int t = wave + kCritWaves * i;
+      if (t >= NT) continue;
+      const int row = k0 + 32 * t + l32;  // pattern B: this lane's row
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        float vb[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int rf = 8 * q + 4 * h + e;
+          const float v = lds_load1(M, (k0 + rf) * ldm + row, 32 * t + l32 > rf && row < npad);
+          vb[e] = (32 * t + l32 == rf) ? 1.0f : v;
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) X[i] = __builtin_amdgcn_mfma_f32_32x32x2f32(vb[e], W[4 * q + e], X[i], 0, 0, 0);
+      }
+#pragma unroll
+      for (int q = 0; q < 4; ++q) {
+        const int rb = k0 + 32 * t + 8 * q + 4 * h;
+        if (colok && rb < npad)
+          *reinterpret_cast<f32x4*>(M + col * ldm + rb) = f32x4{X[i][4 * q + 0], X[i][4 * q + 1], X[i][4 * q + 2],
+                                                                X[i][4 * q + 3]};
+      }
+    }
+  }
+  __syncthreads();
+}
+
+// The far strips (from column c_first) of the panel at k0, one strip per wave,
+// round robin over `nw` waves starting with wave `w0`; this wave is `wave`.
+__device__ __forceinline__ void lds_update_far(float* M, int ldm, int n, int npad, int k0, const float (*Tk)[33],
+                                               int c_first, int wave, int w0, int nw, int h, int l32) {
+  const int nstrips = (n - c_first + 31) >> 5;
+  const int nt = (n - k0 + 31) >> 5;
+  for (int s = wave - w0; s < nstrips; s += nw) {
+    const int c0 = c_first + 32 * s;
+    switch (nt) {
+      case 6: lds_update_strip<6>(M, ldm, n, npad, k0, Tk, c0, h, l32); break;
+      case 5: lds_update_strip<5>(M, ldm, n, npad, k0, Tk, c0, h, l32); break;
+      case 4: lds_update_strip<4>(M, ldm, n, npad, k0, Tk, c0, h, l32); break;
+      case 3: lds_update_strip<3>(M, ldm, n, npad, k0, Tk, c0, h, l32); break;
+      default: lds_update_strip<2>(M, ldm, n, npad, k0, Tk, c0, h, l32); break;
+    }
+  }
+}
+
 }  // namespace
 
 __global__ void __launch_bounds__(kLdsWaves * 64) qr_lds_kernel(const float* __restrict__ A, int64_t as0, int64_t as1,
@@ -189,7 +303,8 @@ __global__ void __launch_bounds__(kLdsWaves * 64) qr_lds_kernel(const float* __r
                                                                 int64_t hs1, int64_t hs2, float* __restrict__ tau,
                                                                 int64_t ts0, int64_t ts1, int n) {
   __shared__ __attribute__((aligned(16))) float M[kLdsMaxN * kLdsMaxLd];
-  __shared__ float Tk[32][33];
+  __shared__ float Tk[2][32][33];  // T of the current and the previous panel
+  __shared__ float Pp[kCritWaves][16][64];
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -248,24 +363,45 @@ __global__ void __launch_bounds__(kLdsWaves * 64) qr_lds_kernel(const float* __r
   }
   __syncthreads();
 
+  // Per 32-column panel at k0 (panel p), two phases:
+  //   B: wave 0 factors the panel (one wave: no barriers in its column loop)
+  //      while waves 1-3 apply the previous panel's transform to the strips
+  //      right of this panel (those columns wait for nothing else);
+  //   A: all waves apply this panel's transform to the next strip, the next
+  //      panel's columns, its tiles split over kCritWaves waves.
+  // Phase B's two parts touch disjoint columns and T buffers (T of panel p
+  // in Tk[p & 1]), so only a barrier between the phases is needed.
   float* tb = tau + b * ts0;
-  for (int k0 = 0; k0 < n; k0 += 32) {
+  for (int k0 = 0, p = 0; k0 < n; k0 += 32, ++p) {
     // lane-derived values are recomputed per panel from an opaque copy of the
     // thread id: hoisted out of this loop they would exceed the SGPR budget
     int t = tid;
     asm volatile("" : "+v"(t));
     const int m = n - k0;
     const int w = m < 32 ? m : 32;
-    if (m > 64) {
-      LdsPanelIO<kLdsWaves> io{M, ldm, k0, Tk, tb, ts1};
-      panel_body<kLdsWaves, 3, 2, true>(io, m, t);
-    } else if (wave == 0) {
-      LdsPanelIO<1> io{M, ldm, k0, Tk, tb, ts1};
-      panel_body<1, 4, 2, true>(io, m, t);
+    const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
+    if (wv == 0) {
+      LdsPanelIO<1> io{M, ldm, k0, Tk[p & 1], tb, ts1};
+      if (m > 64) {
+        panel_body<1, (kLdsMaxN + 15) / 16, 2, true>(io, m, t);
+      } else {
+        panel_body<1, 4, 2, true>(io, m, t);
+      }
+    } else if (k0 > 0 && k0 + 32 < n) {
+      lds_update_far(M, ldm, n, npad, k0 - 32, Tk[(p - 1) & 1], k0 + 32, wv, 1, kLdsWaves - 1, (t >> 5) & 1, t & 31);
     }
     __syncthreads();
-    if (w == 32) lds_update(M, ldm, n, npad, k0, Tk, __builtin_amdgcn_readfirstlane(t >> 6), (t >> 5) & 1, t & 31);
-    __syncthreads();
+    if (w == 32 && k0 + 32 < n) {
+      const int nt = (m + 31) >> 5;
+      const int h = (t >> 5) & 1, l32 = t & 31;
+      switch (nt) {
+        case 6: lds_update_strip_split<6>(M, ldm, n, npad, k0, Tk[p & 1], k0 + 32, wv, h, l32, Pp); break;
+        case 5: lds_update_strip_split<5>(M, ldm, n, npad, k0, Tk[p & 1], k0 + 32, wv, h, l32, Pp); break;
+        case 4: lds_update_strip_split<4>(M, ldm, n, npad, k0, Tk[p & 1], k0 + 32, wv, h, l32, Pp); break;
+        case 3: lds_update_strip_split<3>(M, ldm, n, npad, k0, Tk[p & 1], k0 + 32, wv, h, l32, Pp); break;
+        default: lds_update_strip_split<2>(M, ldm, n, npad, k0, Tk[p & 1], k0 + 32, wv, h, l32, Pp); break;
+      }
+    }
   }
 
   // LDS -> H.  Columns contiguous in H: a wave writes whole columns, lanes
