@@ -165,25 +165,6 @@ __device__ __forceinline__ void lds_update_strip(float* M, int ldm, int n, int n
   }
 }
 
-// Trailing update after the panel at k0: strips of 32 columns round-robin over
-// the waves.  Only a full 32-column panel leaves columns to its right.
-__device__ __forceinline__ void lds_update(float* M, int ldm, int n, int npad, int k0, const float (*Tk)[33], int wave,
-                                           int h, int l32) {
-  const int c_first = k0 + 32;
-  const int nstrips = (n - c_first + 31) >> 5;
-  const int nt = (n - k0 + 31) >> 5;
-  for (int s = wave; s < nstrips; s += kLdsWaves) {
-    const int c0 = c_first + 32 * s;
-    switch (nt) {
-      case 6: lds_update_strip<6>(M, ldm, n, npad, k0, Tk, c0, h, l32); break;
-      case 5: lds_update_strip<5>(M, ldm, n, npad, k0, Tk, c0, h, l32); break;
-      case 4: lds_update_strip<4>(M, ldm, n, npad, k0, Tk, c0, h, l32); break;
-      case 3: lds_update_strip<3>(M, ldm, n, npad, k0, Tk, c0, h, l32); break;
-      default: lds_update_strip<2>(M, ldm, n, npad, k0, Tk, c0, h, l32); break;
-    }
-  }
-}
-
 // The next strip's update after a panel (the critical path), its tiles split
 // over the first kCritWaves waves (wave w takes tiles w, w + kCritWaves, ...):
 // each forms the partial P of its tiles, the partials meet in LDS (summed in
