@@ -33,17 +33,26 @@ namespace fastqr {
 namespace {
 
 // Partial-product layout: one 32x32 block = 16 accumulator registers x 64
-// lanes, register-major, so each lane reads and writes 16 strided floats and
-// every access instruction is one coalesced 256-byte row.
+// lanes, quad-major: registers 4q .. 4q+3 of lane l at floats 256 q + 4 l ..
+// +3, so every access instruction moves one contiguous KiB, 16 bytes per lane
+// (a wave can hold at most 63 loads in flight: with 16-byte loads that is
+// 16 blocks).
+__device__ __forceinline__ int acc_off(int j, int lane) { return 256 * (j >> 2) + 4 * lane + (j & 3); }
+
 __device__ __forceinline__ void store_acc(float* __restrict__ dst, const f32x16& v, int lane) {
 #pragma unroll
-  for (int j = 0; j < 16; ++j) dst[j * 64 + lane] = v[j];
+  for (int q = 0; q < 4; ++q)
+    *reinterpret_cast<f32x4*>(dst + acc_off(4 * q, lane)) = f32x4{v[4 * q], v[4 * q + 1], v[4 * q + 2], v[4 * q + 3]};
 }
 
 __device__ __forceinline__ f32x16 load_acc(const float* __restrict__ src, int lane) {
   f32x16 v;
 #pragma unroll
-  for (int j = 0; j < 16; ++j) v[j] = src[j * 64 + lane];
+  for (int q = 0; q < 4; ++q) {
+    const f32x4 x = *reinterpret_cast<const f32x4*>(src + acc_off(4 * q, lane));
+#pragma unroll
+    for (int i = 0; i < 4; ++i) v[4 * q + i] = x[i];
+  }
   return v;
 }
 
@@ -189,9 +198,9 @@ __global__ void __launch_bounds__(1024) wyr_tg_kernel(const float* __restrict__ 
 #pragma unroll
   for (int u = 0; u < kG; ++u) {
     const int idx = tid + u * 1024;
-    const int lane = idx & 63, j = (idx >> 6) & 15, pair = idx >> 10;
+    const int pair = idx >> 10;
     const int blk = pair % nblk, s = pair / nblk;
-    gv[u] = (idx < nblk * nblk * 1024) ? Gsum[((b * kWyrMaxBlk + blk) * kWyrMaxBlk + s) * 1024 + j * 64 + lane] : 0.0f;
+    gv[u] = (idx < nblk * nblk * 1024) ? Gsum[((b * kWyrMaxBlk + blk) * kWyrMaxBlk + s) * 1024 + (idx & 1023)] : 0.0f;
   }
   // the panels' T factors on the diagonal (nb * nb <= 1024: one element per
   // thread and panel)
@@ -206,7 +215,8 @@ __global__ void __launch_bounds__(1024) wyr_tg_kernel(const float* __restrict__ 
 #pragma unroll
   for (int u = 0; u < kG; ++u) {
     const int idx = tid + u * 1024;
-    const int lane = idx & 63, j = (idx >> 6) & 15, pair = idx >> 10;
+    // float idx & 1023 of the block holds register j of lane `lane` (acc_off)
+    const int lane = (idx >> 2) & 63, j = 4 * ((idx >> 8) & 3) + (idx & 3), pair = idx >> 10;
     const int blk = pair % nblk, s = pair / nblk;
     if (idx < nblk * nblk * 1024) Gs[32 * blk + acc_row(j, lane >> 5)][32 * s + (lane & 31)] = gv[u];
   }
@@ -310,19 +320,29 @@ __global__ void __launch_bounds__(kSumWaves * 64) wyr_w_kernel(const float* __re
 }
 
 // W of one strip formed by a single wave (the fused variant of the apply
-// kernel): the row-block partials summed in row-block order, four loads in
-// flight, then W = -T^T P as in wyr_w_kernel.
+// kernel): the row-block partials summed in row-block order, then W = -T^T P
+// as in wyr_w_kernel.  These launches hold one wave per CU or fewer, so the
+// wave spends registers on latency: up to 16 partials (4 KiB each) are in
+// flight at once (a 4096-row narrow update sums 32 of them).
 template <int NBLK>
 __device__ __forceinline__ void wave_form_w(f32x16 (&W)[NBLK], const float* __restrict__ Ppart, int64_t b, int s,
                                             int nstrips, int nrb, const float* __restrict__ Tb, int ldt, int k,
                                             int lane) {
   const int h = lane >> 5, l32 = lane & 31;
+  constexpr int kInFlight = NBLK == 1 ? 16 : 8;
   f32x16 P[NBLK];
 #pragma unroll
   for (int blk = 0; blk < NBLK; ++blk) {
 #pragma unroll
     for (int j = 0; j < 16; ++j) P[blk][j] = 0.0f;
     int rb = 0;
+    for (; rb + kInFlight <= nrb; rb += kInFlight) {
+      f32x16 v[kInFlight];
+#pragma unroll
+      for (int u = 0; u < kInFlight; ++u) v[u] = load_acc(Ppart + pp_index(b, s, rb + u, blk, nstrips, nrb), lane);
+#pragma unroll
+      for (int u = 0; u < kInFlight; ++u) P[blk] += v[u];
+    }
     for (; rb + 3 < nrb; rb += 4) {
       f32x16 v[4];
 #pragma unroll
