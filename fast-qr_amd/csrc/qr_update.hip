@@ -180,7 +180,8 @@ __global__ void __launch_bounds__(kSumWaves * 64) wyr_reduce_kernel(const float*
 }
 
 // Group T (k x k, leading dimension kWyrTgLd) from the Gram matrix (Gsum) and
-// the panels' T factors (q panels of width nb in workspace slots slot0 ..).
+// the panels' T factors (q panels of width nb, 16 or 32, in workspace slots
+// slot0 ..).
 __global__ void __launch_bounds__(1024) wyr_tg_kernel(const float* __restrict__ Gsum, const float* __restrict__ Tws,
                                                       int slot0, int q, int nb, int k, float* __restrict__ Tg,
                                                       int hi) {
@@ -225,40 +226,43 @@ __global__ void __launch_bounds__(1024) wyr_tg_kernel(const float* __restrict__ 
 #pragma unroll
   for (int i = 0; i < kWyrMaxK / 16; ++i) {
     const int r = tid / nb, c = tid % nb;
-    if (i < q && tid < nb * nb && i * nb + r < k && i * nb + c < k) Ts[i * nb + r][i * nb + c] = tv[i];
+    if (i < q && tid < nb * nb && r <= c && i * nb + r < k && i * nb + c < k) Ts[i * nb + r][i * nb + c] = tv[i];
   }
   __syncthreads();
-  // T join, one panel at a time; the dot products run over four partial sums
-  // so their LDS reads overlap
-  for (int j = 1; j < q; ++j) {
-    const int c0 = j * nb;
-    if (c0 >= k) break;
-    // Mt = G[0:c0, c0:c0+nb] T_j
-    for (int idx = tid; idx < c0 * nb; idx += 1024) {
-      const int r = idx / nb, c = idx % nb;
-      float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      int p = 0;
-      for (; p + 3 <= c; p += 4) {
+  // T join, one panel at a time, on v_mfma_f32_16x16x4f32 with both operands
+  // read from LDS (lane l supplies A(l % 16, l / 16) and B(l / 16, l % 16);
+  // accumulator register i of lane l is C(4 (l / 16) + i, l % 16)), one 16 x 16
+  // output tile per wave and round:
+  //   Mt = G[0:c0, c0:c0+nb] T_j,   T[0:c0, c0:c0+nb] = -T[0:c0, 0:c0] Mt.
+  // Ts is zero below its diagonal and beyond k, so the products run over
+  // whole 4-deep slices without masks (nb and c0 are multiples of 16).
+  {
+    const int wave = tid >> 6, lane = tid & 63;
+    const int li = lane & 15, lk = lane >> 4;
+    for (int j = 1; j < q; ++j) {
+      const int c0 = j * nb;
+      if (c0 >= k) break;
+      const int tc = nb / 16, ntile = (c0 / 16) * tc;
+      for (int t = wave; t < ntile; t += 16) {
+        const int r0 = 16 * (t / tc), cc = 16 * (t % tc);
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int p = 0; p < nb; p += 4)
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Gs[r0 + li][c0 + p + lk], Ts[c0 + p + lk][c0 + cc + li], acc, 0,
+                                                     0, 0);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) a[u] = fmaf(Gs[r][c0 + p + u], Ts[c0 + p + u][c0 + c], a[u]);
+        for (int i = 0; i < 4; ++i) Mt[r0 + 4 * lk + i][cc + li] = acc[i];
       }
-      for (; p <= c; ++p) a[0] = fmaf(Gs[r][c0 + p], Ts[c0 + p][c0 + c], a[0]);
-      Mt[r][c] = (a[0] + a[1]) + (a[2] + a[3]);
-    }
-    __syncthreads();
-    // T[0:c0, c0:c0+nb] = -T[0:c0, 0:c0] Mt   (T upper triangular)
-    for (int idx = tid; idx < c0 * nb; idx += 1024) {
-      const int r = idx / nb, c = idx % nb;
-      float a[4] = {0.0f, 0.0f, 0.0f, 0.0f};
-      int p = r;
-      for (; p + 4 <= c0; p += 4) {
+      __syncthreads();
+      for (int t = wave; t < ntile; t += 16) {
+        const int r0 = 16 * (t / tc), cc = 16 * (t % tc);
+        f32x4 acc = {0.0f, 0.0f, 0.0f, 0.0f};
+        for (int p = r0; p < c0; p += 4)  // T(r, p) = 0 for p < r
+          acc = __builtin_amdgcn_mfma_f32_16x16x4f32(Ts[r0 + li][p + lk], Mt[p + lk][cc + li], acc, 0, 0, 0);
 #pragma unroll
-        for (int u = 0; u < 4; ++u) a[u] = fmaf(Ts[r][p + u], Mt[p + u][c], a[u]);
+        for (int i = 0; i < 4; ++i) Ts[r0 + 4 * lk + i][c0 + cc + li] = -acc[i];
       }
-      for (; p < c0; ++p) a[0] = fmaf(Ts[r][p], Mt[p][c], a[0]);
-      Ts[r][c0 + c] = -((a[0] + a[1]) + (a[2] + a[3]));
+      __syncthreads();
     }
-    __syncthreads();
   }
   float* Tb = Tg + b * kWyrTgStride;
   for (int idx = tid; idx < kWyrMaxK * kWyrMaxK; idx += 1024) {
@@ -452,6 +456,7 @@ size_t wyr_workspace_floats(int64_t batch, int n) {
 hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
   const int m = c.n - c.kv;
   if (c.c_end <= c.c_begin || m <= 0 || c.k <= 0 || c.k > kWyrMaxK) return hipSuccess;
+  if (c.gram && (c.nb % 16 != 0 || c.nb > 32 || c.q * c.nb > kWyrMaxK)) return hipErrorInvalidValue;  // the T join's tiles
   const int nblk = (c.k + 31) / 32;
   const int nrb = (m + c.rows_per_blk - 1) / c.rows_per_blk;
   const int nstrips = (c.c_end - c.c_begin + 31) / 32;
