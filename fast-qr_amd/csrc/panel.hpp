@@ -135,6 +135,28 @@ __device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
 
 }  // namespace
 
+// The LDS a panel factorisation works in (NW waves, NBLK 16-column blocks).
+// It does not depend on the tile count, so a kernel that factors panels of
+// several heights with forms of different tile counts gives them one copy
+// (panel_body_lds); panel_body declares its own.
+template <int NW, int NBLK>
+struct PanelLds {
+  static constexpr int NWR = NW > 1 ? NW : 2;
+  static constexpr int NPAIR = NBLK > 1 ? NBLK / 2 : 1;
+  static constexpr int NW2 = NBLK > 1 ? NW : 1;
+  static constexpr int PCH = NBLK > 4 ? 4 : (NBLK > 1 ? NBLK - 1 : 1);
+  // red[parity][column][wave]: per-wave partials (sum, row j) of one column step
+  __attribute__((aligned(16))) float2 red[2][16][NWR];
+  // T of each 32-column slot (blocks 2p and 2p+1): [[T_2p, T_2p,2p+1], [0, T_2p+1]]
+  float Ts[NPAIR][32][33];
+  float Gs[16][17];
+  float Mt[16][17];
+  // block updates: partial products of up to PCH later blocks are summed over
+  // the waves in one LDS round
+  __attribute__((aligned(16))) f32x4 Pp[NW2][PCH][64];
+  float Vt[NW2][16][17];
+};
+
 // Factor the panel described by `io` (m rows, up to 16 * NBLK columns) with NW
 // waves (threads 0 .. NW*64-1 of the workgroup), TPW 16-row tiles per wave
 // (rows covered: 16 * NW * TPW), NBLK 16-column blocks.  VEC: rows are loaded
@@ -144,8 +166,9 @@ __device__ __forceinline__ f32x4 mfma16(float a, float b, f32x4 c) {
 // (a caller that factors many panels in one kernel passes it through an
 // opaque copy, so that the lane masks derived from it are recomputed per
 // panel instead of being held live across the caller's loop).
+// L: the panel's LDS, which the caller may share between forms.
 template <int NW, int TPW, int NBLK, bool VEC, class IO>
-__device__ __forceinline__ void panel_body(IO& io, int m, int tid) {
+__device__ __forceinline__ void panel_body_lds(IO& io, int m, int tid, PanelLds<NW, NBLK>& L) {
   static_assert(NW == 1 || NW % 2 == 0, "wave count");
   static_assert(NBLK == 1 || NBLK == 2 || NBLK == 4 || NBLK == 8, "16-, 32-, 64- or 128-column panels");
   static_assert(NW * TPW >= NBLK, "the panel's diagonal tiles must exist");
@@ -156,20 +179,14 @@ __device__ __forceinline__ void panel_body(IO& io, int m, int tid) {
   const int kq = lane >> 4;
   const int cn = lane & 15;
 
-  constexpr int NWR = NW > 1 ? NW : 2;
-  // red[parity][column][wave]: per-wave partials (sum, row j) of one column step
-  __shared__ __attribute__((aligned(16))) float2 red[2][16][NWR];
-  // T of each 32-column slot (blocks 2p and 2p+1): [[T_2p, T_2p,2p+1], [0, T_2p+1]]
-  constexpr int NPAIR = NBLK > 1 ? NBLK / 2 : 1;
-  __shared__ float Ts[NPAIR][32][33];
-  __shared__ float Gs[16][17];
-  __shared__ float Mt[16][17];
-  // block updates: partial products of up to PCH later blocks are summed over
-  // the waves in one LDS round
-  constexpr int NW2 = NBLK > 1 ? NW : 1;
-  constexpr int PCH = NBLK > 4 ? 4 : (NBLK > 1 ? NBLK - 1 : 1);
-  __shared__ f32x4 Pp[NW2][PCH][64];
-  __shared__ float Vt[NW2][16][17];
+  constexpr int NPAIR = PanelLds<NW, NBLK>::NPAIR;
+  constexpr int PCH = PanelLds<NW, NBLK>::PCH;
+  auto& red = L.red;
+  auto& Ts = L.Ts;
+  auto& Gs = L.Gs;
+  auto& Mt = L.Mt;
+  auto& Pp = L.Pp;
+  auto& Vt = L.Vt;
   for (int idx = tid; idx < NPAIR * 32 * 33; idx += NW * 64) (&Ts[0][0][0])[idx] = 0.0f;
 
   f32x4 X[NBLK][TPW];
@@ -468,6 +485,12 @@ __device__ __forceinline__ void panel_body(IO& io, int m, int tid) {
       if (c < w) io.store_tau(c, my_tau[blk]);
     }
   }
+}
+
+template <int NW, int TPW, int NBLK, bool VEC, class IO>
+__device__ __forceinline__ void panel_body(IO& io, int m, int tid) {
+  __shared__ PanelLds<NW, NBLK> L;
+  panel_body_lds<NW, TPW, NBLK, VEC>(io, m, tid, L);
 }
 
 }  // namespace fastqr

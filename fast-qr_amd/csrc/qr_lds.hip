@@ -286,6 +286,7 @@ __global__ void __launch_bounds__(kLdsWaves * 64) qr_lds_kernel(const float* __r
   __shared__ __attribute__((aligned(16))) float M[kLdsMaxN * kLdsMaxLd];
   __shared__ float Tk[2][32][33];  // T of the current and the previous panel
   __shared__ float Pp[kCritWaves][16][64];
+  __shared__ PanelLds<1, 2> Lp;  // shared by the panel forms below
   const int64_t b = blockIdx.x;
   const int tid = threadIdx.x;
   const int wave = tid >> 6;
@@ -362,11 +363,19 @@ __global__ void __launch_bounds__(kLdsWaves * 64) qr_lds_kernel(const float* __r
     const int w = m < 32 ? m : 32;
     const int wv = __builtin_amdgcn_readfirstlane(t >> 6);
     if (wv == 0) {
+      // one form per height class: the column loop runs over every tile of
+      // the form, so a form no taller than the panel saves the masked tiles
       LdsPanelIO<1> io{M, ldm, k0, Tk[p & 1], tb, ts1};
-      if (m > 64) {
-        panel_body<1, (kLdsMaxN + 15) / 16, 2, true>(io, m, t);
+      if (m > 144) {
+        panel_body_lds<1, (kLdsMaxN + 15) / 16, 2, true>(io, m, t, Lp);
+      } else if (m > 112) {
+        panel_body_lds<1, 9, 2, true>(io, m, t, Lp);
+      } else if (m > 80) {
+        panel_body_lds<1, 7, 2, true>(io, m, t, Lp);
+      } else if (m > 64) {
+        panel_body_lds<1, 5, 2, true>(io, m, t, Lp);
       } else {
-        panel_body<1, 4, 2, true>(io, m, t);
+        panel_body_lds<1, 4, 2, true>(io, m, t, Lp);
       }
     } else if (k0 > 0 && k0 + 32 < n) {
       lds_update_far(M, ldm, n, npad, k0 - 32, Tk[(p - 1) & 1], k0 + 32, wv, 1, kLdsWaves - 1, (t >> 5) & 1, t & 31);
