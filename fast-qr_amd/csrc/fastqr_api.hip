@@ -400,7 +400,10 @@ int geqrf_impl(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a
   // updates run on the row-split kernels keep one transform per launch over
   // the rest of the group (those kernels join several transforms only with a
   // group T).
-  auto run_panels = [&](const Group& G, hipStream_t st) -> hipError_t {
+  // a_first: the group's columns right of its first panel are not in H yet
+  // (row-major input, only the first panel copied): each narrow update reads
+  // the next panel's columns from A, their first touch.
+  auto run_panels = [&](const Group& G, hipStream_t st, bool a_first = false) -> hipError_t {
     const bool left_looking = !(wyr_narrow && ni - G.g0 > kWyrNarrowMinRows);
     for (int pk = G.g0; pk < G.g_end; pk += G.pw) {
       const double m = ni - pk;
@@ -421,7 +424,7 @@ int geqrf_impl(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a
         const double mg = ni - G.g0;
         err = timed(kUpdate, bd * fl, bd * (8.0 * mg * (c1 - c0) + 4.0 * mg * (c0 - G.g0)), st, [&] {
           return fastqr::launch_wy_update(H, batch, h_s0, h_s2, Tws, ni, G.g0, kTw, G.slot_base, nwy, c0, c1, vec,
-                                          true, 0, st);
+                                          true, 0, st, false, a_first ? A : nullptr, a_s0, a_s1);
         });
         if (err != hipSuccess) return err;
       } else if (c0 < G.g_end) {
@@ -501,7 +504,13 @@ int geqrf_impl(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a
   const int c_first = aux ? groups[0].g_end : ni;
   const bool from_a = aux && !same && a_s2 == 1 && a_s1 >= n &&
                       4 * ((n - 1) * a_s1 + n) < ((int64_t)1 << 31);
-  if ((e = copy_cols(0, c_first)) != hipSuccess) return hip_fail(e, "copy launch");
+  // With left-looking narrow updates in the first group, only its first
+  // panel's columns are copied: the narrow updates read the next panels'
+  // columns from A (the copy is on the critical path before the first panel;
+  // 640 x 512: 128 columns 52 us, 32 columns 13 us).
+  const bool first_from_a =
+      from_a && !(wyr_narrow && ni - groups[0].g0 > kWyrNarrowMinRows) && groups[0].pw < groups[0].g_end;
+  if ((e = copy_cols(0, first_from_a ? groups[0].pw : c_first)) != hipSuccess) return hip_fail(e, "copy launch");
   if (!aux) {
     for (int g = 0; g < ngroups; ++g) {
       const Group& G = groups[g];
@@ -528,7 +537,7 @@ int geqrf_impl(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a
   hipEvent_t ev = record(stream);  // the side stream must not run ahead of work already queued on `stream`
   if (!ev) return fail(FASTQR_EINVAL, "cannot record HIP events");
   if ((e = hipStreamWaitEvent(side, ev, 0)) != hipSuccess) return hip_fail(e, "stream join");
-  if ((e = run_panels(groups[0], side)) != hipSuccess) return hip_fail(e, "panel launch");
+  if ((e = run_panels(groups[0], side, first_from_a)) != hipSuccess) return hip_fail(e, "panel launch");
   // Four workgroups per CU keep the copy at HBM speed and leave the CUs' other
   // slots to the first group's panels: uncapped, its tens of thousands of
   // small workgroups fill every CU and the panels wait for the copy to drain

@@ -25,9 +25,10 @@ namespace fastqr {
 // Copy modes: element loads (any strides), 16-byte row segments transposed
 // through LDS (row-major source), 16-byte column segments (column-major).
 constexpr int kCopyScalar = 0, kCopyRowVec = 1, kCopyColVec = 2;
-// One 64 x 64 tile (row block ti, column block tj) of matrix b.
+// One 64 x 64 tile (row block ti, column block tj) of matrix b; columns >= c1
+// are left alone.
 __device__ __forceinline__ void copy_tile(const float* __restrict__ A, int64_t as0, int64_t as1, int64_t as2,
-                                          float* __restrict__ H, int64_t hs0, int64_t ldh, int n, int mode,
+                                          float* __restrict__ H, int64_t hs0, int64_t ldh, int n, int c1, int mode,
                                           int64_t b, int ti, int tj, float (*tile)[65]) {
   const float* Ab = A + b * as0;
   float* Hb = H + b * hs0;
@@ -42,13 +43,13 @@ __device__ __forceinline__ void copy_tile(const float* __restrict__ A, int64_t a
     for (int k = 0; k < 4; ++k) {
       const int j = (tid >> 4) + 16 * k;
       const int gi = ti * 64 + i4, gj = tj * 64 + j;
-      if (gi < n && gj < n) v[k] = *reinterpret_cast<const f32x4*>(Ab + (int64_t)gj * as2 + gi);
+      if (gi < n && gj < c1) v[k] = *reinterpret_cast<const f32x4*>(Ab + (int64_t)gj * as2 + gi);
     }
 #pragma unroll
     for (int k = 0; k < 4; ++k) {
       const int j = (tid >> 4) + 16 * k;
       const int gi = ti * 64 + i4, gj = tj * 64 + j;
-      if (gi < n && gj < n) *reinterpret_cast<f32x4*>(Hb + (int64_t)gj * ldh + gi) = v[k];
+      if (gi < n && gj < c1) *reinterpret_cast<f32x4*>(Hb + (int64_t)gj * ldh + gi) = v[k];
     }
     return;
   }
@@ -61,7 +62,7 @@ __device__ __forceinline__ void copy_tile(const float* __restrict__ A, int64_t a
     for (int k = 0; k < 4; ++k) {
       const int i = (tid >> 4) + 16 * k;
       const int gi = ti * 64 + i, gj = tj * 64 + c4;
-      v[k] = (gi < n && gj < n) ? *reinterpret_cast<const f32x4*>(Ab + (int64_t)gi * as1 + gj)
+      v[k] = (gi < n && gj < c1) ? *reinterpret_cast<const f32x4*>(Ab + (int64_t)gi * as1 + gj)
                                 : f32x4{0.0f, 0.0f, 0.0f, 0.0f};
     }
 #pragma unroll
@@ -75,7 +76,7 @@ __device__ __forceinline__ void copy_tile(const float* __restrict__ A, int64_t a
     for (int k = 0; k < 4; ++k) {
       const int j = (tid >> 4) + 16 * k;
       const int gi = ti * 64 + c4, gj = tj * 64 + j;
-      if (gi < n && gj < n)
+      if (gi < n && gj < c1)
         *reinterpret_cast<f32x4*>(Hb + (int64_t)gj * ldh + gi) =
             f32x4{tile[c4][j], tile[c4 + 1][j], tile[c4 + 2][j], tile[c4 + 3][j]};
     }
@@ -86,20 +87,20 @@ __device__ __forceinline__ void copy_tile(const float* __restrict__ A, int64_t a
     for (int idx = tid; idx < 64 * 64; idx += 256) {
       const int i = idx >> 6, j = idx & 63;
       const int gi = ti * 64 + i, gj = tj * 64 + j;
-      tile[i][j] = (gi < n && gj < n) ? Ab[gi * as1 + gj * as2] : 0.0f;
+      tile[i][j] = (gi < n && gj < c1) ? Ab[gi * as1 + gj * as2] : 0.0f;
     }
   } else {
     for (int idx = tid; idx < 64 * 64; idx += 256) {
       const int j = idx >> 6, i = idx & 63;
       const int gi = ti * 64 + i, gj = tj * 64 + j;
-      tile[i][j] = (gi < n && gj < n) ? Ab[gi + gj * as2] : 0.0f;
+      tile[i][j] = (gi < n && gj < c1) ? Ab[gi + gj * as2] : 0.0f;
     }
   }
   __syncthreads();
   for (int idx = tid; idx < 64 * 64; idx += 256) {
     const int j = idx >> 6, i = idx & 63;
     const int gi = ti * 64 + i, gj = tj * 64 + j;
-    if (gi < n && gj < n) Hb[(int64_t)gj * ldh + gi] = tile[i][j];
+    if (gi < n && gj < c1) Hb[(int64_t)gj * ldh + gi] = tile[i][j];
   }
 }
 
@@ -110,14 +111,14 @@ __device__ __forceinline__ void copy_tile(const float* __restrict__ A, int64_t a
 __global__ void __launch_bounds__(256) copy_to_colmajor_kernel(const float* __restrict__ A, int64_t as0,
                                                                 int64_t as1, int64_t as2,
                                                                 float* __restrict__ H, int64_t hs0,
-                                                                int64_t ldh, int n, int ntile, int ntj, int tj0,
-                                                                int mode, int64_t total) {
+                                                                int64_t ldh, int n, int c1, int ntile, int ntj,
+                                                                int tj0, int mode, int64_t total) {
   __shared__ float tile[64][65];
   const int per_matrix = ntile * ntj;
   for (int64_t L = blockIdx.x; L < total; L += gridDim.x) {
     const int64_t b = L / per_matrix;
     const int t = (int)(L - b * per_matrix);
-    copy_tile(A, as0, as1, as2, H, hs0, ldh, n, mode, b, t % ntile, tj0 + t / ntile, tile);
+    copy_tile(A, as0, as1, as2, H, hs0, ldh, n, c1, mode, b, t % ntile, tj0 + t / ntile, tile);
     __syncthreads();  // the next tile rewrites `tile`
   }
 }
@@ -384,7 +385,7 @@ hipError_t launch_copy_colmajor(const float* A, int64_t batch, int n, int64_t as
   int64_t grid = total < ((int64_t)1 << 30) ? total : ((int64_t)1 << 30);
   if (max_wgs > 0 && grid > max_wgs) grid = max_wgs;
   hipLaunchKernelGGL(copy_to_colmajor_kernel, dim3((unsigned)grid), dim3(256), 0, stream, A, as0, as1, as2, H, hs0, ldh,
-                     n, ntile, ntj, tj0, mode, total);
+                     n, c1, ntile, ntj, tj0, mode, total);
   return hipGetLastError();
 }
 
