@@ -466,7 +466,14 @@ int geqrf_impl(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a
   // the narrow update after each panel (one workgroup per matrix and strip)
   // runs beside the wide update too; the wide update has slack (measured on
   // MI355X: 8 x 2048 5% faster; eight CUs per matrix gain nothing more).
-  DeviceAux* aux = (ngroups > 2 && !single_stream) ? device_aux() : nullptr;
+  // Small matrices run every launch on the caller's stream: their trailing
+  // updates are short, and the side stream's event hand-offs cost more than
+  // the overlap gains (measured on MI355X, side stream -> one stream: 40 x 352
+  // 363 -> 343 us, 40 x 320 315 -> 272, 40 x 448 483 -> 455, 256 x 352 567 ->
+  // 558, 640 x 256 593 -> 581; but 40 x 512 561 -> 579 and 640 x 352 1,075 ->
+  // 1,125).
+  const bool one_stream = single_stream || n <= 256 || (n <= 448 && batch <= 256);
+  DeviceAux* aux = (ngroups > 2 && !one_stream) ? device_aux() : nullptr;
   int num_cus = 0, dev = 0;
   if (!aux && ngroups > 2) {
     num_cus = 0;  // one stream: the wide update has the whole GPU
