@@ -116,6 +116,7 @@ KIND_BOUND = {
     "wave64": ("hbm", PEAK_HBM_GBS, "GB/s"),
     "lds": ("hbm", PEAK_HBM_GBS, "GB/s"),
 }
+ONE_WG_PER_MATRIX = ("panel", "lds", "wave64")
 KIND_KERNEL = {
     "update": "wy_update_kernel (trailing update A2 -= V T^T V^T A2, v_mfma_f32_32x32x2f32)",
     "update_rowsplit": "wyr_* (row-split trailing update of tall matrices: partial V^T X, T, W, apply)",
@@ -744,11 +745,19 @@ def main() -> int:
     roof_by_kind = {}
     if kernels:
         agg = {}
+        # one workgroup per matrix (panel, LDS and wave64 kernels): a launch
+        # occupies min(batch, CUs) CUs, so each is also set against the peak of
+        # the CUs it can use (kernel time weighted by that share of the GPU)
+        n_cus = torch.cuda.get_device_properties(0).multi_processor_count
+        batch_of = {s.label: s.batch for _, s in shapes}
+        occ_ms = {}
         for label, kd in kernels.items():
             for kname, st in kd.items():
                 a = agg.setdefault(kname, {"launches": 0, "ms": 0.0, "flops": 0.0, "bytes": 0.0})
                 for f in a:
                     a[f] += st.get(f, 0)
+                share = min(batch_of.get(label, n_cus), n_cus) / n_cus
+                occ_ms[kname] = occ_ms.get(kname, 0.0) + st.get("ms", 0.0) * share
         tot_ms = sum(a["ms"] for a in agg.values()) or 1.0
         for kname, a in agg.items():
             if not a["launches"] or a["ms"] <= 0:
@@ -770,6 +779,9 @@ def main() -> int:
                 "work_per_launch": work / a["launches"],
                 "time_share": round(a["ms"] / tot_ms, 3),
             }
+            if kname in ONE_WG_PER_MATRIX and occ_ms.get(kname, 0.0) > 0:
+                occ = work / (occ_ms[kname] * 1e-3) / (1e12 if unit == "TFLOP/s" else 1e9)
+                roof_by_kind[kname]["frac_of_occupied_cus"] = round(occ / peak, 4)
         if roof_by_kind:
             dom = max(roof_by_kind, key=lambda k: roof_by_kind[k]["time_share"])
             roof = dict(roof_by_kind[dom])
