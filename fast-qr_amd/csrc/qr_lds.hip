@@ -15,7 +15,7 @@
 //     right of this panel;
 //   * the panel's compact-WY transform is applied to the next strip with
 //     v_mfma_f32_32x32x2f32, every operand read from LDS,
-//     X <- X - V (T^T (V^T X)), its tiles split over three waves.
+//     X <- X - V (T^T (V^T X)), its tiles split over the four waves.
 // Rows between n and LDM stay zero throughout (the reflectors never touch
 // them), so 4-row groups need no per-row masking.
 #include "kernels.hpp"
@@ -26,7 +26,7 @@ namespace fastqr {
 namespace {
 
 constexpr int kLdsWaves = 4;
-constexpr int kCritWaves = 3;  // waves sharing the next strip's update (LDS for their partials)
+constexpr int kCritWaves = 4;  // waves sharing the next strip's update (LDS for their partials)
 constexpr int kLdsMaxTiles = (kLdsMaxN + 31) / 32;          // 32-row MFMA tiles of a strip
 constexpr int kLdsMaxLd = ((kLdsMaxN + 3) & ~3) + 4;         // leading dimension for n = kLdsMaxN
 
