@@ -187,7 +187,8 @@ struct WaveQR {
 
   template <int... J>
   __device__ __forceinline__ void run(int n, seq<J...>) {
-    // steps J < n in order; the fold stops at the first J >= n
+    // steps J < n in order (n here: the number of steps); the fold stops at
+    // the first J >= n
     (void)((J < n ? (step<J>(), true) : false) && ...);
   }
 };
@@ -228,7 +229,10 @@ __global__ void __launch_bounds__(64) qr_wave_kernel(const float* __restrict__ A
     q.inv[tr] = 0.0f;
   }
 
-  q.run(n, typename make_seq<16 * NT>::type{});
+  // steps 0 .. n-2: the last column has no rows below its diagonal, so its
+  // reflector is the identity (tau 0, R_nn = alpha), which the registers
+  // already hold (tau and the scale start at 0; LAPACK's slarfg(1, ...) alike)
+  q.run(n - 1, typename make_seq<16 * NT>::type{});
   q.scale_reflectors();
 
   float* Hb = H + b * hs0;
