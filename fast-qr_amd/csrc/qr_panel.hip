@@ -125,16 +125,24 @@ hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float
       nw = 8, tpw = 14;
     } else if (m <= 2048) {
       nw = 8, tpw = 16;
+    } else if (m <= 2304) {
+      nw = 8, tpw = 18;
     } else if (m <= 2560) {
       nw = 8, tpw = 20;
+    } else if (m <= 2816) {
+      nw = 8, tpw = 22;
     } else if (m <= 3072) {
       nw = 8, tpw = 24;
     }
   } else if (nb == 16) {
     if (m <= 2048) {
       nw = 8, tpw = 16;
+    } else if (m <= 3328) {
+      nw = 8, tpw = 26;
     } else if (m <= 3584) {
       nw = 8, tpw = 28;
+    } else if (m <= 3840) {
+      nw = 8, tpw = 30;
     } else if (m <= 4096) {
       nw = 8, tpw = 32;
     }

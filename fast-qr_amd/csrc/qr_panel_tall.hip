@@ -18,6 +18,10 @@ FASTQR_PANEL_LAUNCHER(panel_launch_tall) {
   FASTQR_PANEL(8, 14, 2)
   FASTQR_PANEL(8, 20, 2)
   FASTQR_PANEL(8, 28, 1)
+  FASTQR_PANEL(8, 18, 2)
+  FASTQR_PANEL(8, 22, 2)
+  FASTQR_PANEL(8, 26, 1)
+  FASTQR_PANEL(8, 30, 1)
   return hipSuccess;
 }
 
