@@ -501,16 +501,16 @@ int geqrf_impl(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a
     });
   };
 
-  // With the side stream, only the first group's columns are copied before
-  // its panels start.  A row-major input is not copied any further: the first
-  // group's look-ahead and wide updates, the first kernels that touch the
-  // other columns, read them from A and write them to H (one read of A and no
-  // extra pass over H; a copy beside the first group's panels takes HBM and
-  // CU slots from them).  Other layouts copy the rest on the caller's stream
-  // beside those panels, ahead of the first look-ahead update.
-  const int c_first = aux ? groups[0].g_end : ni;
-  const bool from_a = aux && !same && a_s2 == 1 && a_s1 >= n &&
-                      4 * ((n - 1) * a_s1 + n) < ((int64_t)1 << 31);
+  // Only the first group's columns are copied before its panels start.  A
+  // row-major input is not copied any further: the first group's look-ahead
+  // and wide updates, the first kernels that touch the other columns, read
+  // them from A and write them to H (one read of A and no extra pass over H;
+  // a copy beside the first group's panels takes HBM and CU slots from them).
+  // Other layouts copy the rest: with the side stream on the caller's stream
+  // beside those panels, ahead of the first look-ahead update; on one stream
+  // up front.
+  const bool from_a = !same && a_s2 == 1 && a_s1 >= n && 4 * ((n - 1) * a_s1 + n) < ((int64_t)1 << 31);
+  const int c_first = (aux || from_a) ? groups[0].g_end : ni;
   // With left-looking narrow updates in the first group, only its first
   // panel's columns are copied: the narrow updates read the next panels'
   // columns from A (the copy is on the critical path before the first panel;
@@ -521,8 +521,8 @@ int geqrf_impl(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a
   if (!aux) {
     for (int g = 0; g < ngroups; ++g) {
       const Group& G = groups[g];
-      e = run_panels(G, stream);
-      if (e == hipSuccess) e = run_update(G, G.g_end, ni, false, stream);
+      e = run_panels(G, stream, g == 0 && first_from_a);
+      if (e == hipSuccess) e = run_update(G, G.g_end, ni, false, stream, g == 0 && from_a);
       if (e != hipSuccess) return hip_fail(e, "blocked launch");
     }
     return FASTQR_OK;
