@@ -10,6 +10,7 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <algorithm>
 #include <atomic>
 #include <vector>
 
@@ -35,6 +36,8 @@ int hip_fail(hipError_t e, const char* what) {
 }
 
 constexpr int64_t kMaxN = 4096;
+// Largest n of the mixed-precision variant (its panels and Q^T C calls).
+constexpr int64_t kMixedMaxN = 2048;
 constexpr int kWaveMaxN = 64;
 // Tall matrices use the row-split trailing update (a 32-column strip of more
 // than 2048 rows does not fit in one workgroup's registers, and small batches
@@ -814,6 +817,146 @@ int fastqr_geqrf_f32_noalloc(const float* A, int64_t batch, int64_t n, int64_t a
   }
   return geqrf_impl(A, batch, n, a_s0, a_s1, a_s2, H, h_s0, h_s1, h_s2, tau, tau_s0, tau_s1, ws,
                     need > 0 ? (size_t)FASTQR_NOALLOC_SCRATCH_BYTES : 0, true, stream_ptr);
+}
+
+}  // extern "C"
+
+// ---- mixed-precision variant (tools/blocked_qr_reference.py:193-262) ------
+
+namespace {
+
+// Workspace of fastqr_geqrf_mixed_f32, 256-byte aligned regions: the panel T
+// slots, the repair buffer C (column-major, leading dimension n: A's columns
+// k.. for R maintenance, the panel's for the refresh) and the workspace of
+// the fp32 Q^T C calls that recompute them.
+struct MixedLayout {
+  size_t t_bytes = 0, c_bytes = 0, q_bytes = 0;
+  int64_t c_cols = 0;
+  size_t total() const { return t_bytes + c_bytes + q_bytes; }
+};
+
+size_t round256(size_t b) { return (b + 255) & ~(size_t)255; }
+
+bool mixed_layout(int64_t batch, int64_t n, int64_t pw, int flags, MixedLayout* L) {
+  if (batch <= 0 || n <= 0 || n > kMixedMaxN || batch > fastqr::kMaxGridY || (pw != 16 && pw != 32) ||
+      (flags & ~(FASTQR_MIXED_R_MAINTENANCE | FASTQR_MIXED_PANEL_REFRESH)) != 0)
+    return false;
+  L->t_bytes = round256((size_t)batch * fastqr::kMaxSlots * 32 * 32 * sizeof(float));
+  const bool rm = flags & FASTQR_MIXED_R_MAINTENANCE, pr = flags & FASTQR_MIXED_PANEL_REFRESH;
+  L->c_cols = rm ? n : pr ? pw : 0;
+  L->c_bytes = round256((size_t)batch * n * L->c_cols * sizeof(float));
+  size_t q = 0;
+  for (int64_t k = 0; k < n; k += pw) {
+    const int64_t w = n - k < pw ? n - k : pw;
+    if (pr && k > 0) q = std::max(q, fastqr_ormqr_workspace_bytes(batch, n, k, w));
+    if (rm) q = std::max(q, fastqr_ormqr_workspace_bytes(batch, n, k + w, n - k));
+  }
+  L->q_bytes = round256(q);
+  return true;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t fastqr_geqrf_mixed_workspace_bytes(int64_t batch, int64_t n, int64_t panel_width, int flags) {
+  MixedLayout L;
+  return mixed_layout(batch, n, panel_width, flags, &L) ? L.total() : 0;
+}
+
+int fastqr_geqrf_mixed_f32(const float* A, int64_t batch, int64_t n, int64_t a_s0, int64_t a_s1, int64_t a_s2,
+                           float* H, int64_t h_s0, int64_t h_s1, int64_t h_s2, float* tau, int64_t tau_s0,
+                           int64_t tau_s1, int64_t panel_width, int precision, int flags, void* workspace,
+                           size_t workspace_bytes, void* stream_ptr) {
+  g_last_error[0] = '\0';
+  if (g_forced_error != 0) {
+    const int code = g_forced_error;
+    g_forced_error = 0;
+    return fail(code, "forced error %d (test hook)", code);
+  }
+  if (batch < 0 || n < 0) return fail(FASTQR_EINVAL, "batch and n must be non-negative (got %lld, %lld)",
+                                      (long long)batch, (long long)n);
+  if (panel_width != 16 && panel_width != 32)
+    return fail(FASTQR_EINVAL, "panel_width must be 16 or 32 (got %lld)", (long long)panel_width);
+  if (precision < FASTQR_PREC_FP32 || precision > FASTQR_PREC_BF16_INPUT)
+    return fail(FASTQR_EINVAL, "precision must be one of FASTQR_PREC_* (got %d)", precision);
+  if ((flags & ~(FASTQR_MIXED_R_MAINTENANCE | FASTQR_MIXED_PANEL_REFRESH)) != 0)
+    return fail(FASTQR_EINVAL, "unknown flags 0x%x", flags);
+  if (batch == 0 || n == 0) return FASTQR_OK;
+  if (n > kMixedMaxN) return fail(FASTQR_EINVAL, "n=%lld exceeds the mixed variant's maximum %lld", (long long)n,
+                                  (long long)kMixedMaxN);
+  if (batch > fastqr::kMaxGridY) return fail(FASTQR_EINVAL, "batch=%lld exceeds %lld", (long long)batch,
+                                             (long long)fastqr::kMaxGridY);
+  if (!A || !H || !tau) return fail(FASTQR_EINVAL, "A, H and tau must be non-null device pointers");
+  if (a_s0 < 0 || a_s1 < 0 || a_s2 < 0 || h_s0 < 0 || h_s2 < 0 || tau_s0 < 0 || tau_s1 < 0)
+    return fail(FASTQR_EINVAL, "negative strides are not supported");
+  if (batch > 1 && (h_s0 == 0 || tau_s0 == 0))
+    return fail(FASTQR_EINVAL, "H and tau batch strides must be non-zero when batch > 1");
+  if (n > 1 && tau_s1 == 0) return fail(FASTQR_EINVAL, "tau column stride must be non-zero");
+  if (h_s1 != 1 || h_s2 < n)
+    return fail(FASTQR_ELAYOUT, "H must have contiguous columns (stride (*, 1, >=n)); got (%lld, %lld, %lld)",
+                (long long)h_s0, (long long)h_s1, (long long)h_s2);
+  if (h_s2 * n * 4 >= (int64_t)1 << 31)
+    return fail(FASTQR_ELAYOUT, "one matrix of H spans %lld bytes; at most 2 GiB are addressed",
+                (long long)(h_s2 * n * 4));
+  if (batch > 1 && h_s0 < h_s2 * n)
+    return fail(FASTQR_ELAYOUT, "H batch stride %lld smaller than one matrix (%lld)", (long long)h_s0,
+                (long long)(h_s2 * n));
+  const int64_t h_span = span_elems(batch, n, h_s0, 1, h_s2);
+  if (ranges_overlap(A, span_elems(batch, n, a_s0, a_s1, a_s2), H, h_span))
+    return fail(FASTQR_EOVERLAP, "A and H overlap (the repair steps read A again)");
+  if (ranges_overlap(tau, span_elems(batch, n, tau_s0, tau_s1, 0), H, h_span))
+    return fail(FASTQR_EOVERLAP, "tau and H overlap");
+  MixedLayout L;
+  mixed_layout(batch, n, panel_width, flags, &L);
+  if (workspace_bytes < L.total() || workspace == nullptr)
+    return fail(FASTQR_EWORKSPACE, "workspace of %zu bytes required, %zu given", L.total(), workspace_bytes);
+  if (((uintptr_t)workspace & 255) != 0) return fail(FASTQR_EWORKSPACE, "workspace must be 256-byte aligned");
+
+  hipStream_t stream = (hipStream_t)stream_ptr;
+  float* Tws = (float*)workspace;
+  float* C = (float*)((char*)workspace + L.t_bytes);
+  void* qws = (char*)workspace + L.t_bytes + L.c_bytes;
+  const int ni = (int)n, pw = (int)panel_width;
+  const int64_t c_s0 = n * L.c_cols;
+  const bool vec = ((uintptr_t)H % 16 == 0) && (h_s0 % 4 == 0) && (h_s2 % 4 == 0) && (n % 4 == 0);
+  const bool rm = flags & FASTQR_MIXED_R_MAINTENANCE, pr = flags & FASTQR_MIXED_PANEL_REFRESH;
+  hipError_t e = fastqr::launch_copy_colmajor(A, batch, ni, a_s0, a_s1, a_s2, H, h_s0, h_s2, 0, ni, stream);
+  if (e != hipSuccess) return hip_fail(e, "copy launch");
+  for (int k = 0; k < ni; k += pw) {
+    const int w = ni - k < pw ? ni - k : pw;
+    if (pr && k > 0) {
+      // panel rows k.. <- rows k.. of Q_k^T A[:, k:k+w], Q_k = H_0 ... H_{k-1}, in fp32
+      if ((e = fastqr::launch_block_copy(A + k * a_s2, batch, a_s0, a_s1, a_s2, C, c_s0, 1, n, ni, w, 0, 0, false,
+                                         stream)) != hipSuccess)
+        return hip_fail(e, "refresh copy launch");
+      int rc = fastqr_ormqr_f32(H, batch, n, k, h_s0, 1, h_s2, tau, tau_s0, tau_s1, C, w, c_s0, 1, n, 1, qws,
+                                L.q_bytes, stream_ptr);
+      if (rc != FASTQR_OK) return rc;
+      if ((e = fastqr::launch_block_copy(C + k, batch, c_s0, 1, n, H + k * h_s2 + k, h_s0, 1, h_s2, ni - k, w, k, k,
+                                         false, stream)) != hipSuccess)
+        return hip_fail(e, "refresh copy launch");
+    }
+    if ((e = fastqr::launch_panel(H, batch, h_s0, h_s2, tau, tau_s0, tau_s1, Tws, ni, k, pw, ni - k, 0, vec,
+                                  stream)) != hipSuccess)
+      return hip_fail(e, "panel launch");
+    if (k + w < ni &&
+        (e = fastqr::launch_mixed_update(precision, H, batch, h_s0, h_s2, Tws, ni, k, w, k + w, stream)) != hipSuccess)
+      return hip_fail(e, "mixed update launch");
+    if (rm) {
+      // rows k .. k+w-1 of columns k.. (upper triangle) <- Q_{k+w}^T A[:, k:], in fp32
+      if ((e = fastqr::launch_block_copy(A + k * a_s2, batch, a_s0, a_s1, a_s2, C, c_s0, 1, n, ni, ni - k, 0, 0,
+                                         false, stream)) != hipSuccess)
+        return hip_fail(e, "repair copy launch");
+      int rc = fastqr_ormqr_f32(H, batch, n, k + w, h_s0, 1, h_s2, tau, tau_s0, tau_s1, C, n - k, c_s0, 1, n, 1, qws,
+                                L.q_bytes, stream_ptr);
+      if (rc != FASTQR_OK) return rc;
+      if ((e = fastqr::launch_block_copy(C + k, batch, c_s0, 1, n, H + k * h_s2 + k, h_s0, 1, h_s2, w, ni - k, k, k,
+                                         true, stream)) != hipSuccess)
+        return hip_fail(e, "repair copy launch");
+    }
+  }
+  return FASTQR_OK;
 }
 
 }  // extern "C"

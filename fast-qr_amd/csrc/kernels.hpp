@@ -50,6 +50,19 @@ hipError_t launch_panel(float* H, int64_t batch, int64_t hs0, int64_t ldh, float
 // to kernels on another stream; kWyLeaveOneSlot caps it at one workgroup per
 // CU fewer than fit, leaving a slot on every CU.
 constexpr int kWyLeaveOneSlot = -1;
+
+// Mixed-precision variant (qr_mixed.hip).  Operand precision of its trailing
+// update (the values of FASTQR_PREC_* in the C header).
+constexpr int kPrecF32 = 0, kPrecTf32 = 1, kPrecF16 = 2, kPrecBf16 = 3;
+// Columns [c_begin, n), rows [k0, n) <- minus V r(r(T)^T r(r(V)^T r(X))) for
+// the panel of width w at column k0 (its T in workspace slot 0).
+hipError_t launch_mixed_update(int prec, float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n,
+                               int k0, int w, int c_begin, hipStream_t stream);
+// dst[b, dr0 + i, dc0 + j] = src[b, i, j], i < rows, j < cols (pointers at
+// their first element); `upper`: only where dr0 + i <= dc0 + j.
+hipError_t launch_block_copy(const float* src, int64_t batch, int64_t s0, int64_t s1, int64_t s2, float* dst,
+                             int64_t d0, int64_t d1, int64_t d2, int rows, int cols, int dr0, int dc0, bool upper,
+                             hipStream_t stream);
 // With A (row-major, leading dimension lda, batch stride as0) the columns
 // [c_begin, c_end) are read from A instead of H and written to H (their first
 // update, when the blocked path did not copy them); strips of at most 2048

@@ -84,6 +84,37 @@ static PyObject* py_ormqr(PyObject* self, PyObject* const* args, Py_ssize_t narg
   return PyLong_FromLong(rc);
 }
 
+/* geqrf_mixed(A, batch, n, as0, as1, as2, H, hs0, hs1, hs2, tau, ts0, ts1, panel_width, precision, flags, ws,
+ *             ws_bytes, stream) -> int */
+static PyObject* py_geqrf_mixed(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
+  (void)self;
+  if (nargs != 19) {
+    PyErr_SetString(PyExc_TypeError, "geqrf_mixed expects 19 integer arguments");
+    return NULL;
+  }
+  void *A, *H, *tau, *ws, *stream;
+  int64_t b, n, as0, as1, as2, hs0, hs1, hs2, ts0, ts1, pw, prec, flags, wsb;
+  if (as_ptr(args[0], &A) || as_i64(args[1], &b) || as_i64(args[2], &n) || as_i64(args[3], &as0) ||
+      as_i64(args[4], &as1) || as_i64(args[5], &as2) || as_ptr(args[6], &H) || as_i64(args[7], &hs0) ||
+      as_i64(args[8], &hs1) || as_i64(args[9], &hs2) || as_ptr(args[10], &tau) || as_i64(args[11], &ts0) ||
+      as_i64(args[12], &ts1) || as_i64(args[13], &pw) || as_i64(args[14], &prec) || as_i64(args[15], &flags) ||
+      as_ptr(args[16], &ws) || as_i64(args[17], &wsb) || as_ptr(args[18], &stream))
+    return NULL;
+  const int rc = fastqr_geqrf_mixed_f32((const float*)A, b, n, as0, as1, as2, (float*)H, hs0, hs1, hs2, (float*)tau,
+                                        ts0, ts1, pw, (int)prec, (int)flags, ws, (size_t)wsb, stream);
+  return PyLong_FromLong(rc);
+}
+
+static PyObject* py_geqrf_mixed_workspace_bytes(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
+  (void)self;
+  int64_t b, n, pw, flags;
+  if (nargs != 4 || as_i64(args[0], &b) || as_i64(args[1], &n) || as_i64(args[2], &pw) || as_i64(args[3], &flags)) {
+    if (!PyErr_Occurred()) PyErr_SetString(PyExc_TypeError, "geqrf_mixed_workspace_bytes(batch, n, panel_width, flags)");
+    return NULL;
+  }
+  return PyLong_FromSize_t(fastqr_geqrf_mixed_workspace_bytes(b, n, pw, (int)flags));
+}
+
 static PyObject* py_ormqr_workspace_bytes(PyObject* self, PyObject* const* args, Py_ssize_t nargs) {
   (void)self;
   int64_t b, m, r, k;
@@ -142,6 +173,10 @@ static PyMethodDef methods[] = {
     {"ormqr", (PyCFunction)(void (*)(void))py_ormqr, METH_FASTCALL, "fastqr_ormqr_f32 over raw pointers"},
     {"ormqr_workspace_bytes", (PyCFunction)(void (*)(void))py_ormqr_workspace_bytes, METH_FASTCALL,
      "fastqr_ormqr_workspace_bytes"},
+    {"geqrf_mixed", (PyCFunction)(void (*)(void))py_geqrf_mixed, METH_FASTCALL,
+     "fastqr_geqrf_mixed_f32 over raw pointers"},
+    {"geqrf_mixed_workspace_bytes", (PyCFunction)(void (*)(void))py_geqrf_mixed_workspace_bytes, METH_FASTCALL,
+     "fastqr_geqrf_mixed_workspace_bytes"},
     {"last_error", py_last_error, METH_NOARGS, "fastqr_last_error"},
     {"path_name", py_path_name, METH_O, "fastqr_path_name"},
     {"version", py_version, METH_NOARGS, "fastqr_version"},

@@ -22,6 +22,13 @@ FASTQR_EWORKSPACE = -2
 FASTQR_ELAYOUT = -3
 FASTQR_EOVERLAP = -4
 FASTQR_ETESTHOOK = -99
+# operand precision and repair flags of fastqr_geqrf_mixed_f32 (FASTQR_PREC_*, FASTQR_MIXED_*)
+FASTQR_PREC_FP32 = 0
+FASTQR_PREC_TF32_INPUT = 1
+FASTQR_PREC_FP16_INPUT = 2
+FASTQR_PREC_BF16_INPUT = 3
+FASTQR_MIXED_R_MAINTENANCE = 1
+FASTQR_MIXED_PANEL_REFRESH = 2
 # size of the static device scratch of fastqr_geqrf_f32_noalloc (FASTQR_NOALLOC_SCRATCH_BYTES)
 NOALLOC_SCRATCH_BYTES = 32 << 20
 
@@ -34,6 +41,8 @@ EXPORTED_SYMBOLS = (
     "fastqr_orgqr_workspace_bytes",
     "fastqr_ormqr_f32",
     "fastqr_ormqr_workspace_bytes",
+    "fastqr_geqrf_mixed_f32",
+    "fastqr_geqrf_mixed_workspace_bytes",
     "fastqr_path_name",
     "fastqr_last_error",
     "fastqr_version",
@@ -90,6 +99,11 @@ def cdll() -> ctypes.CDLL:
         lib.fastqr_ormqr_workspace_bytes.argtypes = [i64, i64, i64, i64]
         lib.fastqr_ormqr_workspace_bytes.restype = sz
         lib.fastqr_workspace_bytes.restype = sz
+        lib.fastqr_geqrf_mixed_f32.argtypes = [vp, i64, i64, i64, i64, i64, vp, i64, i64, i64, vp, i64, i64, i64,
+                                               ctypes.c_int, ctypes.c_int, vp, sz, vp]
+        lib.fastqr_geqrf_mixed_f32.restype = ctypes.c_int
+        lib.fastqr_geqrf_mixed_workspace_bytes.argtypes = [i64, i64, i64, ctypes.c_int]
+        lib.fastqr_geqrf_mixed_workspace_bytes.restype = sz
         lib.fastqr_path_name.argtypes = [i64]
         lib.fastqr_path_name.restype = ctypes.c_char_p
         lib.fastqr_last_error.argtypes = []

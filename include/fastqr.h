@@ -172,6 +172,50 @@ int fastqr_ormqr_f32(const float* H, int64_t batch, int64_t m, int64_t r,
 /* Workspace bytes fastqr_ormqr_f32 needs for (batch, m, r, k). */
 size_t fastqr_ormqr_workspace_bytes(int64_t batch, int64_t m, int64_t r, int64_t k);
 
+/* Operand precision of the mixed-precision variant's trailing update. */
+#define FASTQR_PREC_FP32 0        /* no rounding (fp32 MFMA)                      */
+#define FASTQR_PREC_TF32_INPUT 1  /* operands rounded to 10 mantissa bits          */
+#define FASTQR_PREC_FP16_INPUT 2  /* operands in fp16 (fp16 MFMA, fp32 accumulate) */
+#define FASTQR_PREC_BF16_INPUT 3  /* operands in bf16 (bf16 MFMA, fp32 accumulate) */
+/* Repair steps of the mixed-precision variant (bit flags). */
+#define FASTQR_MIXED_R_MAINTENANCE 1  /* r_maintenance_mode="panel-prefix" */
+#define FASTQR_MIXED_PANEL_REFRESH 2  /* panel_refresh_mode="prefix"       */
+
+/*
+ * Blocked QR with a reduced-precision trailing update and optional fp32
+ * repair: an experimental, separately labelled variant, not the fp32 path of
+ * fastqr_geqrf_f32.  Replaces the reference's prototype
+ * blocked_geqrf_reference(data, panel_width, update_mode="compact-wy",
+ * precision_mode, r_maintenance_mode, panel_refresh_mode)
+ * (tools/blocked_qr_reference.py:193-262) and its CUDA kernels
+ * blocked512_panel_refresh_kernel / blocked512_panel_r_repair_kernel with
+ * update_operand_352 (submissions/candidate.py:539-554, 2240-2402).
+ *
+ * Per panel of `panel_width` columns at column k: with PANEL_REFRESH (k > 0)
+ * the panel's rows k.. are recomputed in fp32 from A by the k reflectors
+ * before it; the panel is factored in fp32; the trailing columns get
+ * X - r(V) r(r(T)^T r(r(V)^T r(X))), r() the rounding of `precision`; with
+ * R_MAINTENANCE rows k .. k+w-1 of columns k.. (upper triangle) are
+ * recomputed in fp32 from A by the first k+w reflectors.  Without repair a
+ * reduced precision fails the reference checker's factor gate; with both
+ * repairs the result meets the fp32 gates.
+ *
+ * Arguments as fastqr_geqrf_f32, plus panel_width (16 or 32), precision
+ * (FASTQR_PREC_*) and flags (FASTQR_MIXED_*).  A is read again by the repair
+ * steps, so A and H must not overlap.  1 <= n <= 2048, batch <= 65535.
+ * workspace: fastqr_geqrf_mixed_workspace_bytes(batch, n, panel_width, flags)
+ * bytes, 256-byte aligned.
+ */
+int fastqr_geqrf_mixed_f32(const float* A, int64_t batch, int64_t n,
+                           int64_t a_s0, int64_t a_s1, int64_t a_s2,
+                           float* H, int64_t h_s0, int64_t h_s1, int64_t h_s2,
+                           float* tau, int64_t tau_s0, int64_t tau_s1,
+                           int64_t panel_width, int precision, int flags,
+                           void* workspace, size_t workspace_bytes, void* stream);
+
+/* Workspace bytes fastqr_geqrf_mixed_f32 needs (0 for invalid arguments). */
+size_t fastqr_geqrf_mixed_workspace_bytes(int64_t batch, int64_t n, int64_t panel_width, int flags);
+
 /*
  * Name of the kernel path fastqr_geqrf_f32 takes for size n ("wave64",
  * "lds", "blocked"); the reference's shape switch is custom_kernel

@@ -99,6 +99,31 @@ def official_check(a, h, tau) -> tuple[bool, str]:
     )
 
 
+def diagnose(a, h, tau) -> dict:
+    """Scaled residuals of (H, tau), restating tools/diagnose.py:22-75.
+
+    factor = ||R - Q^T A||_1, tri = ||tril(Q^T A, -1)||_1 and reconstruction
+    = ||QR - A||_1, each over eps32 * n * ||A||_1; orth = ||Q^T Q - I||_1 over
+    eps32 * n; the maximum over the batch of each.
+    """
+    a = _t(a)
+    h = _t(h)
+    tau = _t(tau)
+    n = a.shape[-1]
+    q64 = torch.linalg.householder_product(h, tau).double()
+    r64 = torch.triu(h).double()
+    a64 = a.double()
+    projected = q64.transpose(-1, -2) @ a64
+    scale = _l1(a64).clamp_min(1e-30) * EPS32 * n
+    eye = torch.eye(n, dtype=torch.float64).expand_as(projected)
+    return {
+        "factor_scaled_max": float((_l1(r64 - projected) / scale).max()),
+        "tri_scaled_max": float((_l1(torch.tril(projected, -1)) / scale).max()),
+        "orth_scaled_max": float((_l1(q64.transpose(-1, -2) @ q64 - eye) / (EPS32 * n)).max()),
+        "reconstruction_scaled_max": float((_l1(q64 @ r64 - a64) / scale).max()),
+    }
+
+
 @dataclass
 class GateReport:
     ok: bool
