@@ -90,9 +90,15 @@ def parse_args():
     p.add_argument("--summarize-counters", metavar="PMC_DIR",
                    help="print per-kernel MFMA / VALU utilisation from a rocprofv3 --pmc run of this script with "
                         + " ".join(UTIL_COUNTERS) + ", and exit")
+    p.add_argument("--trace-flat", action="store_true",
+                   help="with --summarize-trace: one table over all calls (for a --mixed trace)")
     p.add_argument("--summarize-trace", metavar="KERNEL_TRACE_CSV",
                    help="print per-kernel statistics of a rocprofv3 --kernel-trace run of this script, split into "
                         "the geqrf calls and the householder_product calls, and exit")
+    p.add_argument("--mixed", action="store_true",
+                   help="time the mixed-precision variant (blocked_geqrf_mixed) per operand precision, without "
+                        "and with its fp32 repairs, beside custom_kernel on the same inputs; prints its own "
+                        "JSON line (not the headline)")
     p.add_argument("--traffic-file", default=str(ROOT / "profiles" / TRAFFIC_SUMMARY),
                    help="committed traffic summary that fills roofline.traffic")
     return p.parse_args()
@@ -283,23 +289,26 @@ def summarize_counters(directory: str) -> str:
 GEQRF_ONLY = ("copy_to_colmajor", "qr_wave_kernel", "qr_lds_kernel", "panel_kernel")
 
 
-def summarize_trace(path: str) -> str:
+def summarize_trace(path: str, flat: bool = False) -> str:
     """Markdown: per kernel, calls and average/min/max duration, for the geqrf
-    calls and the householder_product calls of a bench.py kernel trace."""
+    calls and the householder_product calls of a bench.py kernel trace (with
+    ``flat``, one table over every call: the --mixed leg)."""
     import csv
 
     rows = sorted(csv.DictReader(open(path)), key=lambda r: int(r["Dispatch_Id"]))
-    stats = {"geqrf": {}, "householder_product": {}}
-    phase = "geqrf"
+    stats = {"all": {}} if flat else {"geqrf": {}, "householder_product": {}}
+    phase = "all" if flat else "geqrf"
     for r in rows:
         name = r["Kernel_Name"]
         if "fastqr::" not in name:
             continue
-        if "orgqr_" in name:
+        if flat:
+            pass
+        elif "orgqr_" in name:
             phase = "householder_product"
         elif any(k in name for k in GEQRF_ONLY):
             phase = "geqrf"
-        short = name.replace("void ", "").split("(")[0]
+        short = name.replace("void ", "").replace("(anonymous namespace)::", "").split("(")[0]
         d = (int(r["End_Timestamp"]) - int(r["Start_Timestamp"])) / 1e3
         ent = stats[phase].setdefault(short, [0, 0.0, float("inf"), 0.0])
         ent[0] += 1
@@ -423,6 +432,58 @@ def run_eval_contract(args) -> int:
     return 0 if ok_all else 3
 
 
+# Shapes of the mixed-precision leg (the variant stops at n = 2048).
+MIXED_SHAPES = (("C2", 40, 352), ("C3", 640, 512), ("C4", 60, 1024))
+
+
+def run_mixed(args, dev) -> int:
+    """One JSON line: µs/call of blocked_geqrf_mixed per precision mode, bare and
+    repaired, next to custom_kernel, and whether each passes the official gates
+    (first four matrices)."""
+    import torch
+
+    import fastqr
+    from fastqr import mixed
+    from oracle import checker
+
+    def timed(fn, reps):
+        fn()
+        torch.cuda.synchronize()
+        e0 = torch.cuda.Event(enable_timing=True)
+        e1 = torch.cuda.Event(enable_timing=True)
+        e0.record()
+        for _ in range(reps):
+            fn()
+        e1.record()
+        torch.cuda.synchronize()
+        return round(e0.elapsed_time(e1) * 1e3 / reps, 1)
+
+    shapes = {}
+    for name, b, n in MIXED_SHAPES:
+        g = torch.Generator().manual_seed(1000 + n)
+        a_cpu = torch.randn((b, n, n), generator=g, dtype=torch.float32)
+        a = a_cpu.to(dev)
+        row = {"custom_kernel": timed(lambda: fastqr.custom_kernel(a), args.steps)}
+        gates = {}
+        for mode in mixed.PRECISION_MODES:
+            for repaired in (False, True):
+                kw = dict(precision_mode=mode)
+                if repaired:
+                    kw.update(r_maintenance_mode="panel-prefix", panel_refresh_mode="prefix")
+                key = mode + ("+repair" if repaired else "")
+                row[key] = timed(lambda: mixed.blocked_geqrf_mixed(a, **kw), max(1, args.steps // (5 if repaired else 1)))
+                h, tau = mixed.blocked_geqrf_mixed(a[:4], **kw)
+                gates[key] = checker.official_check(a_cpu[:4], h.cpu(), tau.cpu())[0]
+                log(f"[mixed] {name} {b}x{n} {key}: {row[key]} us/call, gates {'pass' if gates[key] else 'fail'}")
+        shapes[f"{b}x{n}"] = {"config": name, "us_per_call": row, "official_gates_first4": gates}
+    print(json.dumps({
+        "metric": "mixed-precision variant µs/call per operand precision (not the headline)",
+        "unit": "us/call", "higher_is_better": False, "n_gpus": 1, "steps": args.steps,
+        "data": "synthetic N(0,1)", "config": {"workload": "mixed-precision blocked QR", "shapes": shapes},
+    }), flush=True)
+    return 0
+
+
 def main() -> int:
     args = parse_args()
     if args.summarize_traffic:
@@ -432,7 +493,7 @@ def main() -> int:
         print(summarize_counters(args.summarize_counters))
         return 0
     if args.summarize_trace:
-        print(summarize_trace(args.summarize_trace))
+        print(summarize_trace(args.summarize_trace, args.trace_flat))
         return 0
     world = int(os.environ.get("WORLD_SIZE", "1"))
     if args.gpus != 1 or world > 1:
@@ -459,6 +520,8 @@ def main() -> int:
     ncores = len(os.sched_getaffinity(0))
     torch.set_num_threads(ncores)
     fastqr.ext()  # fail loudly if the native library is missing
+    if args.mixed:
+        return run_mixed(args, dev)
     if args.calibrate_copy:
         src = torch.ones(CALIB_BYTES // 4, device=dev)
         dst = torch.empty_like(src)

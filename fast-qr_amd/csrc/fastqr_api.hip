@@ -941,7 +941,7 @@ int fastqr_geqrf_mixed_f32(const float* A, int64_t batch, int64_t n, int64_t a_s
                                   stream)) != hipSuccess)
       return hip_fail(e, "panel launch");
     if (k + w < ni &&
-        (e = fastqr::launch_mixed_update(precision, H, batch, h_s0, h_s2, Tws, ni, k, w, k + w, stream)) != hipSuccess)
+        (e = fastqr::launch_mixed_update(precision, H, batch, h_s0, h_s2, Tws, ni, k, w, k + w, vec, stream)) != hipSuccess)
       return hip_fail(e, "mixed update launch");
     if (rm) {
       // rows k .. k+w-1 of columns k.. (upper triangle) <- Q_{k+w}^T A[:, k:], in fp32

@@ -55,9 +55,10 @@ constexpr int kWyLeaveOneSlot = -1;
 // update (the values of FASTQR_PREC_* in the C header).
 constexpr int kPrecF32 = 0, kPrecTf32 = 1, kPrecF16 = 2, kPrecBf16 = 3;
 // Columns [c_begin, n), rows [k0, n) <- minus V r(r(T)^T r(r(V)^T r(X))) for
-// the panel of width w at column k0 (its T in workspace slot 0).
+// the panel of width w at column k0 (its T in workspace slot 0).  vec: 16-byte
+// column segments (H 16-byte aligned, ldh, batch stride and n multiples of 4).
 hipError_t launch_mixed_update(int prec, float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n,
-                               int k0, int w, int c_begin, hipStream_t stream);
+                               int k0, int w, int c_begin, bool vec, hipStream_t stream);
 // dst[b, dr0 + i, dc0 + j] = src[b, i, j], i < rows, j < cols (pointers at
 // their first element); `upper`: only where dr0 + i <= dc0 + j.
 hipError_t launch_block_copy(const float* src, int64_t batch, int64_t s0, int64_t s1, int64_t s2, float* dst,

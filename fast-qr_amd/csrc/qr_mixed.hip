@@ -91,7 +91,10 @@ constexpr int kMixedWaves = 4;
 // update of columns [c_begin + 32*strip, +32) ∩ [c_begin, n), rows [k0, n),
 // by the panel of width w at column k0 (V below its diagonal in H, T in
 // workspace slot 0 of the matrix).  Wave wv owns the 32-row tiles wv, wv+4, ...
-template <int PREC>
+// Tiles are read in the accumulator layout (lane (h, l32): rows 8s+4h .. +3
+// of column l32, 16 bytes per lane with VEC); the apply phase needs V by
+// rows, which it gets through a per-wave LDS transpose.
+template <int PREC, bool VEC>
 __global__ void __launch_bounds__(kMixedWaves * 64)
 mixed_update_kernel(float* __restrict__ H, int64_t hs0, int ldh, const float* __restrict__ Tws, int n, int k0,
                     int w, int c_begin) {
@@ -106,19 +109,44 @@ mixed_update_kernel(float* __restrict__ H, int64_t hs0, int ldh, const float* __
   const rsrc_t rs = make_rsrc(H + b * hs0, (uint32_t)(4 * (int64_t)ldh * n));
   // element (row r, column c) of the panel-relative block: rows from k0
   auto off = [&](int r, int c) -> uint32_t { return 4u * (uint32_t)((k0 + c) * ldh + k0 + r); };
+  // rows r0 .. r0+3 of column c (VEC: m is a multiple of 4, so r0 < m covers all four)
+  auto load4 = [&](int r0, int c, bool ok) -> f32x4 {
+    if constexpr (VEC) return buf_load4(rs, (ok && r0 < m) ? off(r0, c) : kOffNone);
+    f32x4 v;
+#pragma unroll
+    for (int t = 0; t < 4; ++t) v[t] = buf_load(rs, (ok && r0 + t < m) ? off(r0 + t, c) : kOffNone);
+    return v;
+  };
+  auto store4 = [&](int r0, int c, bool ok, f32x4 v) {
+    if constexpr (VEC) {
+      buf_store4(rs, (ok && r0 < m) ? off(r0, c) : kOffNone, v);
+    } else {
+#pragma unroll
+      for (int t = 0; t < 4; ++t) buf_store(rs, (ok && r0 + t < m) ? off(r0 + t, c) : kOffNone, v[t]);
+    }
+  };
+  // V of tile rt in the accumulator layout: va[4s+t] = V[32 rt + 8s+4h+t][l32]
+  // (zero above the diagonal, one on it, H below; columns >= w zero)
+  auto v_tile = [&](int rt, float (&va)[16]) {
+#pragma unroll
+    for (int s = 0; s < 4; ++s) {
+      const int r0 = 32 * rt + 8 * s + 4 * h;
+      const f32x4 x = load4(r0, l32, l32 < w && r0 + 3 > l32);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) {
+        const int r = r0 + t;
+        va[4 * s + t] = (l32 >= w || r < l32) ? 0.0f : (r == l32 ? 1.0f : x[t]);
+      }
+    }
+  };
 
   __shared__ float Ts[32][33];
   __shared__ float Pp[kMixedWaves][16][64];
+  __shared__ float Vt[kMixedWaves][32][33];
   for (int idx = threadIdx.x; idx < 32 * 32; idx += kMixedWaves * 64) {
     const int r = idx >> 5, c = idx & 31;
     Ts[r][c] = (r < w && c < w) ? Tws[b * kMaxSlots * 1024 + r * 32 + c] : 0.0f;
   }
-
-  // V element (r, c): zero above the diagonal, one on it, H below; columns >= w zero
-  auto v_at = [&](int r, int c, bool ok) -> float {
-    const float x = buf_load(rs, (ok && r > c && c < w && r < m) ? off(r, c) : kOffNone);
-    return (ok && r == c && c < w) ? 1.0f : x;
-  };
 
   // P = V^T X over this wave's tiles
   f32x16 P;
@@ -126,23 +154,24 @@ mixed_update_kernel(float* __restrict__ H, int64_t hs0, int ldh, const float* __
   for (int j = 0; j < 16; ++j) P[j] = 0.0f;
   for (int rt = wave; rt < ntiles; rt += kMixedWaves) {
     float va[16], xb[16];
+    v_tile(rt, va);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int r = 32 * rt + 8 * (j >> 2) + 4 * h + (j & 3);
-      va[j] = v_at(r, l32, true);  // A[l32][row] = V[row][l32]
-      xb[j] = buf_load(rs, (colok && r < m) ? off(r, col - k0) : kOffNone);
+    for (int s = 0; s < 4; ++s) {
+      const f32x4 x = load4(32 * rt + 8 * s + 4 * h, col - k0, colok);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) xb[4 * s + t] = x[t];
     }
-    mma32<PREC>(P, va, xb);
+    mma32<PREC>(P, va, xb);  // A[l32][row] = V[row][l32], B = X
   }
 #pragma unroll
   for (int j = 0; j < 16; ++j) Pp[wave][j][lane] = P[j];
   __syncthreads();
 #pragma unroll
   for (int j = 0; j < 16; ++j) {
-    float s = 0.0f;
+    float sum = 0.0f;
 #pragma unroll
-    for (int wv = 0; wv < kMixedWaves; ++wv) s += Pp[wv][j][lane];
-    P[j] = s;
+    for (int wv = 0; wv < kMixedWaves; ++wv) sum += Pp[wv][j][lane];
+    P[j] = sum;
   }
 
   // M = T^T P: A[l32][kk] = T[kk][l32], B = P in accumulator layout
@@ -160,20 +189,28 @@ mixed_update_kernel(float* __restrict__ H, int64_t hs0, int ldh, const float* __
 #pragma unroll
   for (int j = 0; j < 16; ++j) mb[j] = Mw[j];
 
-  // X <- X - V M, tile by tile: A[l32][kk] = V[row l32][kk]
+  // X <- X - V M, tile by tile: A[l32][kk] = V[row l32][kk], from the
+  // accumulator-layout tile through LDS
   for (int rt = wave; rt < ntiles; rt += kMixedWaves) {
     float va[16];
+    v_tile(rt, va);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) va[j] = v_at(32 * rt + l32, 8 * (j >> 2) + 4 * h + (j & 3), true);
+    for (int j = 0; j < 16; ++j) Vt[wave][8 * (j >> 2) + 4 * h + (j & 3)][l32] = va[j];
+    wave_sync_lds();
+#pragma unroll
+    for (int j = 0; j < 16; ++j) va[j] = Vt[wave][l32][8 * (j >> 2) + 4 * h + (j & 3)];
+    wave_sync_lds();  // this tile's reads before the next tile's writes
     f32x16 D;
 #pragma unroll
     for (int j = 0; j < 16; ++j) D[j] = 0.0f;
     mma32<PREC>(D, va, mb);
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int r = 32 * rt + 8 * (j >> 2) + 4 * h + (j & 3);
-      const uint32_t o = (colok && r < m) ? off(r, col - k0) : kOffNone;
-      buf_store(rs, o, buf_load(rs, o) - D[j]);
+    for (int s = 0; s < 4; ++s) {
+      const int r0 = 32 * rt + 8 * s + 4 * h;
+      f32x4 x = load4(r0, col - k0, colok);
+#pragma unroll
+      for (int t = 0; t < 4; ++t) x[t] -= D[4 * s + t];
+      store4(r0, col - k0, colok, x);
     }
   }
 }
@@ -196,30 +233,36 @@ block_copy_kernel(const float* __restrict__ src, int64_t s0, int64_t s1, int64_t
 }  // namespace
 
 hipError_t launch_mixed_update(int prec, float* H, int64_t batch, int64_t hs0, int64_t ldh, const float* Tws, int n,
-                               int k0, int w, int c_begin, hipStream_t stream) {
+                               int k0, int w, int c_begin, bool vec, hipStream_t stream) {
   if (c_begin >= n || w < 1 || w > 32 || batch < 1 || batch > kMaxGridY) return hipErrorInvalidValue;
+  // the 16-byte form needs 4-row groups that never straddle the last row
+  if (vec && ((n - k0) % 4 != 0 || ldh % 4 != 0 || k0 % 4 != 0)) return hipErrorInvalidValue;
   const dim3 grid((unsigned)((n - c_begin + 31) / 32), (unsigned)batch);
   const dim3 block(kMixedWaves * 64);
+#define FASTQR_MIXED_LAUNCH(P)                                                                                  \
+  if (vec)                                                                                                      \
+    hipLaunchKernelGGL((mixed_update_kernel<P, true>), grid, block, 0, stream, H, hs0, (int)ldh, Tws, n, k0, w,  \
+                       c_begin);                                                                                \
+  else                                                                                                          \
+    hipLaunchKernelGGL((mixed_update_kernel<P, false>), grid, block, 0, stream, H, hs0, (int)ldh, Tws, n, k0, w, \
+                       c_begin);
   switch (prec) {
     case kPrecF32:
-      hipLaunchKernelGGL(mixed_update_kernel<kPrecF32>, grid, block, 0, stream, H, hs0, (int)ldh, Tws, n, k0, w,
-                         c_begin);
+      FASTQR_MIXED_LAUNCH(kPrecF32);
       break;
     case kPrecTf32:
-      hipLaunchKernelGGL(mixed_update_kernel<kPrecTf32>, grid, block, 0, stream, H, hs0, (int)ldh, Tws, n, k0, w,
-                         c_begin);
+      FASTQR_MIXED_LAUNCH(kPrecTf32);
       break;
     case kPrecF16:
-      hipLaunchKernelGGL(mixed_update_kernel<kPrecF16>, grid, block, 0, stream, H, hs0, (int)ldh, Tws, n, k0, w,
-                         c_begin);
+      FASTQR_MIXED_LAUNCH(kPrecF16);
       break;
     case kPrecBf16:
-      hipLaunchKernelGGL(mixed_update_kernel<kPrecBf16>, grid, block, 0, stream, H, hs0, (int)ldh, Tws, n, k0, w,
-                         c_begin);
+      FASTQR_MIXED_LAUNCH(kPrecBf16);
       break;
     default:
       return hipErrorInvalidValue;
   }
+#undef FASTQR_MIXED_LAUNCH
   return hipGetLastError();
 }
 
