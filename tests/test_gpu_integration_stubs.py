@@ -46,7 +46,40 @@ def lib():
     lib.fastqr_ormqr_f32.restype = ctypes.c_int
     lib.fastqr_ormqr_workspace_bytes.argtypes = [i64, i64, i64, i64]
     lib.fastqr_ormqr_workspace_bytes.restype = ctypes.c_size_t
+    lib.fastqr_geqrf_mixed_f32.argtypes = [vp, i64, i64, i64, i64, i64, vp, i64, i64, i64, vp, i64, i64,
+                                           i64, ctypes.c_int, ctypes.c_int, vp, ctypes.c_size_t, vp]
+    lib.fastqr_geqrf_mixed_f32.restype = ctypes.c_int
+    lib.fastqr_geqrf_mixed_workspace_bytes.argtypes = [i64, i64, i64, ctypes.c_int]
+    lib.fastqr_geqrf_mixed_workspace_bytes.restype = ctypes.c_size_t
     return lib
+
+
+def geqrf_mixed(lib, data, h, tau, panel_width, precision, flags):
+    b, n, _ = data.shape
+    ws_bytes = lib.fastqr_geqrf_mixed_workspace_bytes(b, n, panel_width, flags)
+    ws = torch.empty(max(ws_bytes, 1), dtype=torch.uint8, device=data.device)
+    rc = lib.fastqr_geqrf_mixed_f32(data.data_ptr(), b, n, *data.stride(), h.data_ptr(), *h.stride(),
+                                    tau.data_ptr(), *tau.stride(), panel_width, precision, flags,
+                                    ws.data_ptr(), ws_bytes,
+                                    torch.cuda.current_stream(data.device).cuda_stream)
+    if rc != 0:
+        raise RuntimeError(lib.fastqr_last_error().decode())
+
+
+@pytest.mark.parametrize("precision,flags,gates", [(0, 0, True), (3, 0, False), (3, 3, True)])
+def test_mixed_stub_on_device_pointers(cuda, lib, precision, flags, gates):
+    """bf16-input bare fails the gates, with both repairs (flags 3) passes, as
+    the reference's prototype does in tf32 (tests/test_qr_smoke.py:218-258)."""
+    _say(f"[stub mixed] precision={precision} flags={flags}")
+    g = torch.Generator().manual_seed(71)
+    a = torch.randn((3, 96, 96), generator=g, dtype=torch.float32)
+    d = a.to(cuda)
+    h = torch.empty_strided((3, 96, 96), (96 * 96, 1, 96), dtype=torch.float32, device=cuda)
+    tau = torch.empty((3, 96), dtype=torch.float32, device=cuda)
+    geqrf_mixed(lib, d, h, tau, 32, precision, flags)
+    torch.cuda.synchronize()
+    ok, msg = checker.official_check(a, h.cpu(), tau.cpu())
+    assert ok == gates, msg
 
 
 def geqrf(lib, data, h, tau):
