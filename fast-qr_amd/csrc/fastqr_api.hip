@@ -908,7 +908,7 @@ int fastqr_geqrf_mixed_f32(const float* A, int64_t batch, int64_t n, int64_t a_s
   if (ranges_overlap(tau, span_elems(batch, n, tau_s0, tau_s1, 0), H, h_span))
     return fail(FASTQR_EOVERLAP, "tau and H overlap");
   MixedLayout L;
-  mixed_layout(batch, n, panel_width, flags, &L);
+  if (!mixed_layout(batch, n, panel_width, flags, &L)) return fail(FASTQR_EINVAL, "invalid mixed-precision arguments");
   if (workspace_bytes < L.total() || workspace == nullptr)
     return fail(FASTQR_EWORKSPACE, "workspace of %zu bytes required, %zu given", L.total(), workspace_bytes);
   if (((uintptr_t)workspace & 255) != 0) return fail(FASTQR_EWORKSPACE, "workspace must be 256-byte aligned");

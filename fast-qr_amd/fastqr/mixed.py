@@ -26,7 +26,6 @@ from __future__ import annotations
 
 import torch
 
-from . import workspace
 from ._lib import (FASTQR_MIXED_PANEL_REFRESH, FASTQR_MIXED_R_MAINTENANCE, FASTQR_PREC_BF16_INPUT,
                    FASTQR_PREC_FP16_INPUT, FASTQR_PREC_FP32, FASTQR_PREC_TF32_INPUT, FastQRError, ext)
 from .qr import _current_stream_ptr, _validate
@@ -103,7 +102,9 @@ def blocked_geqrf_mixed(
     mod = ext()
     sptr = _current_stream_ptr(idx)
     nbytes = mod.geqrf_mixed_workspace_bytes(b, n, panel_width, flags)
-    ws = workspace.scratch(data.device, sptr, nbytes)
+    # per call, not the shared per-stream scratch: with R maintenance it holds
+    # a copy of the whole batch, which should not stay cached
+    ws = torch.empty(nbytes, dtype=torch.uint8, device=data.device)
     as0, as1, as2 = data.stride()
     rc = mod.geqrf_mixed(data.data_ptr(), b, n, as0, as1, as2, h.data_ptr(), n * n, 1, n, tau.data_ptr(), n, 1,
                          panel_width, _PREC[precision_mode], flags, ws.data_ptr(), ws.numel(), sptr)
