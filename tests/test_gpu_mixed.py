@@ -116,6 +116,22 @@ def test_full_repair_meets_the_fp32_gates(cuda, mode, pw, n):
     assert np.abs(h - ho).max() <= 1e-4 * np.abs(ho).max()
 
 
+@pytest.mark.parametrize("batch,n,pw", [(1, 1, 16), (3, 2, 16), (2, 17, 16), (2, 33, 32), (2, 50, 16)])
+def test_repairs_on_ragged_and_tiny_sizes(cuda, batch, n, pw):
+    """Last panels narrower than the panel width, a single column, and the
+    repairs' copies from a column-major input view."""
+    _say(f"[mixed ragged] batch={batch} n={n} pw={pw}")
+    a = case(batch, n, 1, 40 + n)
+    for src in (a, a.transpose(1, 2).contiguous().transpose(1, 2)):
+        h, tau = run(src, cuda, panel_width=pw, precision_mode="bf16-input", r_maintenance_mode="panel-prefix",
+                     panel_refresh_mode="prefix")
+        ok, msg = checker.official_check(a, h, tau)
+        assert ok, msg
+        ho, to = M.blocked_geqrf_mixed(a, pw, "compact-wy", "bf16-input", "panel-prefix", "prefix")
+        assert np.abs(h - ho).max() <= 1e-4 * max(1.0, np.abs(ho).max())
+        assert np.abs(tau - to).max() <= 1e-4
+
+
 def test_r_maintenance_alone_still_fails(cuda):
     a = case(3, 64, 1, 9)
     h, tau = run(a, cuda, panel_width=16, precision_mode="tf32-input", r_maintenance_mode="panel-prefix")
