@@ -441,6 +441,12 @@ int wyr_rows_per_block(int m, int64_t batch, int cols) {
   const int64_t strips = (cols + 31) / 32;
   int r = 512;
   while (r > 128 && batch * strips * ((m + r - 1) / r) < 1024) r >>= 1;
+  // A batch of a few matrices still under that count at 128 rows: 64-row
+  // blocks (measured on MI355X: 2 x 4096 13.3 -> 12.8 ms; for 8 x 2048 the
+  // longer partial sum of each apply wave outweighs the extra waves).  The
+  // strip bound keeps batch * strips * row blocks within the partial-product
+  // area that wyr_workspace_floats sizes for 128-row blocks.
+  if (batch <= 4 && batch * strips * ((m + 127) / 128) < 1024 && 2 * strips <= m / 64 + 2) r = 64;
   return r;
 }
 
