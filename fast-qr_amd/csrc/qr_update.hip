@@ -72,16 +72,24 @@ __device__ __forceinline__ int64_t pp_index(int64_t b, int s, int rb, int blk, i
 //
 // SEPX: the updated columns are a matrix X of their own (xcols columns,
 // leading dimension ldx, H's rows) (ormqr).  H holds vcols columns.
-template <int NBLK, bool VEC, bool SEPX>
-__global__ void __launch_bounds__(64) wyr_partial_kernel(const float* __restrict__ H, int64_t hs0, int ldh, int n,
-                                                         int kv, int k, int c_begin, int c_end, int gram_end,
-                                                         int rows_per_blk, float* __restrict__ Ppart, int nstrips,
-                                                         int nrb, int hi, const float* __restrict__ X_, int64_t xs0,
-                                                         int ldx, int xcols, int vcols) {
+//
+// PG waves per workgroup, one row block each (rb = PG * blockIdx.y + wave):
+// with PG = 4 the four partials meet in LDS (added in wave order, so the sum
+// is bitwise reproducible) and one partial per group of four row blocks is
+// stored -- whoever forms W then sums a quarter as many (nrp = gridDim.y).
+template <int NBLK, bool VEC, bool SEPX, int PG>
+__global__ void __launch_bounds__(64 * PG) wyr_partial_kernel(const float* __restrict__ H, int64_t hs0, int ldh,
+                                                              int n, int kv, int k, int c_begin, int c_end,
+                                                              int gram_end, int rows_per_blk,
+                                                              float* __restrict__ Ppart, int nstrips, int nrp, int hi,
+                                                              const float* __restrict__ X_, int64_t xs0, int ldx,
+                                                              int xcols, int vcols) {
+  static_assert(PG == 1 || PG == 4, "row blocks per partial");
   if (hi) __builtin_amdgcn_s_setprio(2);
-  const int s = blockIdx.x, rb = blockIdx.y;
+  const int wave = PG == 1 ? 0 : __builtin_amdgcn_readfirstlane((int)threadIdx.x >> 6);
+  const int s = blockIdx.x, rb = PG * (int)blockIdx.y + wave;
   const int64_t b = blockIdx.z;
-  const int lane = threadIdx.x, h = lane >> 5, l32 = lane & 31;
+  const int lane = threadIdx.x & 63, h = lane >> 5, l32 = lane & 31;
   const int col = c_begin + 32 * s + l32;
   const bool colok = col < c_end;
   const bool is_v = !SEPX && c_begin + 32 * s < gram_end;  // strip of the group's own columns: read as V
@@ -129,8 +137,29 @@ __global__ void __launch_bounds__(64) wyr_partial_kernel(const float* __restrict
 #pragma unroll
     for (int blk = 0; blk < NBLK; ++blk) V[blk] = Vn[blk];
   }
+  if constexpr (PG == 1) {
 #pragma unroll
-  for (int blk = 0; blk < NBLK; ++blk) store_acc(Ppart + pp_index(b, s, rb, blk, nstrips, nrb), P[blk], lane);
+    for (int blk = 0; blk < NBLK; ++blk)
+      store_acc(Ppart + pp_index(b, s, (int)blockIdx.y, blk, nstrips, nrp), P[blk], lane);
+  } else {
+    // one reflector block at a time through LDS; wave w adds and stores
+    // register quarter w (one contiguous KiB of the partial's layout)
+    __shared__ __attribute__((aligned(16))) float red[PG][1024];
+#pragma unroll
+    for (int blk = 0; blk < NBLK; ++blk) {
+#pragma unroll
+      for (int q = 0; q < 4; ++q)
+        *reinterpret_cast<f32x4*>(&red[wave][256 * q + 4 * lane]) =
+            f32x4{P[blk][4 * q], P[blk][4 * q + 1], P[blk][4 * q + 2], P[blk][4 * q + 3]};
+      __syncthreads();
+      f32x4 sum = *reinterpret_cast<const f32x4*>(&red[0][256 * wave + 4 * lane]);
+#pragma unroll
+      for (int v = 1; v < PG; ++v) sum += *reinterpret_cast<const f32x4*>(&red[v][256 * wave + 4 * lane]);
+      *reinterpret_cast<f32x4*>(Ppart + pp_index(b, s, (int)blockIdx.y, blk, nstrips, nrp) + 256 * wave + 4 * lane) =
+          sum;
+      __syncthreads();  // every wave's reads before the next block's writes
+    }
+  }
 }
 
 // Sum of the row-block partials of one (strip, reflector block) by the four
@@ -465,19 +494,30 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
   if (c.gram && (c.nb % 16 != 0 || c.nb > 32 || c.q * c.nb > kWyrMaxK)) return hipErrorInvalidValue;  // the T join's tiles
   const int nblk = (c.k + 31) / 32;
   const int nrb = (m + c.rows_per_blk - 1) / c.rows_per_blk;
+  // partials per four row blocks once there are 8 or more: W is formed (by
+  // every apply wave on the critical path) from a quarter as many
+  const int pg = nrb >= 8 ? 4 : 1;
+  const int nrp = (nrb + pg - 1) / pg;
   const int nstrips = (c.c_end - c.c_begin + 31) / 32;
   const int gram_strips = c.gram ? nblk : 0;  // the first strips of [c_begin, c_end) are the group's own columns
   const int gram_end = c.gram ? c.kv + c.k : 0;
   const int hi = c.hi_prio ? 1 : 0;
   float* Ppart = c.scratch;
-  float* Wbuf = c.scratch + (size_t)c.batch * nstrips * nrb * kWyrMaxBlk * 1024;
-  const dim3 gp((unsigned)nstrips, (unsigned)nrb, (unsigned)c.batch);
+  float* Wbuf = c.scratch + (size_t)c.batch * nstrips * nrp * kWyrMaxBlk * 1024;
+  const dim3 gp((unsigned)nstrips, (unsigned)nrp, (unsigned)c.batch);
   const bool sepx = c.X != nullptr;
   const int vcols = c.vcols > 0 ? c.vcols : c.n;
-#define WYR_PARTIAL2(NB_, VEC_, SEPX_)                                                                             \
-  hipLaunchKernelGGL((wyr_partial_kernel<NB_, VEC_, SEPX_>), gp, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv, \
-                     c.k, c.c_begin, c.c_end, gram_end, c.rows_per_blk, Ppart, nstrips, nrb, hi, c.X, c.xs0, c.ldx, \
-                     c.xcols, vcols)
+#define WYR_PARTIAL3(NB_, VEC_, SEPX_, PG_)                                                                       \
+  hipLaunchKernelGGL((wyr_partial_kernel<NB_, VEC_, SEPX_, PG_>), gp, dim3(64 * PG_), 0, stream, c.H, c.hs0, c.ldh, \
+                     c.n, c.kv, c.k, c.c_begin, c.c_end, gram_end, c.rows_per_blk, Ppart, nstrips, nrp, hi, c.X,     \
+                     c.xs0, c.ldx, c.xcols, vcols)
+#define WYR_PARTIAL2(NB_, VEC_, SEPX_)    \
+  do {                                    \
+    if (pg == 4)                          \
+      WYR_PARTIAL3(NB_, VEC_, SEPX_, 4);  \
+    else                                  \
+      WYR_PARTIAL3(NB_, VEC_, SEPX_, 1);  \
+  } while (0)
 #define WYR_PARTIAL(NB_)                                                                                           \
   do {                                                                                                             \
     if (sepx) {                                                                                                    \
@@ -499,6 +539,7 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
   }
 #undef WYR_PARTIAL
 #undef WYR_PARTIAL2
+#undef WYR_PARTIAL3
   hipError_t e = hipGetLastError();
   if (e != hipSuccess) return e;
 
@@ -510,7 +551,7 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
     float* Gsum = Wbuf + (size_t)c.batch * nstrips * kWyrMaxBlk * 1024;
     hipLaunchKernelGGL(wyr_reduce_kernel, dim3((unsigned)gram_strips, (unsigned)nblk, (unsigned)c.batch),
                        dim3(kSumWaves * 64), 0,
-                       stream, Ppart, nstrips, nrb, Gsum, hi);
+                       stream, Ppart, nstrips, nrp, Gsum, hi);
     if ((e = hipGetLastError()) != hipSuccess) return e;
     hipLaunchKernelGGL(wyr_tg_kernel, dim3((unsigned)c.batch), dim3(1024), 0, stream, Gsum, c.Tws, c.slot0, c.q, c.nb,
                        c.k, c.Tg, hi);
@@ -528,19 +569,19 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
   const dim3 gw((unsigned)nx, (unsigned)c.batch);
   if (!fw) switch (nblk) {
     case 1:
-      hipLaunchKernelGGL((wyr_w_kernel<1>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
+      hipLaunchKernelGGL((wyr_w_kernel<1>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrp, gram_strips, Tsrc, t_stride,
                          ldt, c.k, Wbuf, nx, hi, c.t_trans ? 1 : 0);
       break;
     case 2:
-      hipLaunchKernelGGL((wyr_w_kernel<2>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
+      hipLaunchKernelGGL((wyr_w_kernel<2>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrp, gram_strips, Tsrc, t_stride,
                          ldt, c.k, Wbuf, nx, hi, c.t_trans ? 1 : 0);
       break;
     case 3:
-      hipLaunchKernelGGL((wyr_w_kernel<3>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
+      hipLaunchKernelGGL((wyr_w_kernel<3>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrp, gram_strips, Tsrc, t_stride,
                          ldt, c.k, Wbuf, nx, hi, c.t_trans ? 1 : 0);
       break;
     default:
-      hipLaunchKernelGGL((wyr_w_kernel<4>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrb, gram_strips, Tsrc, t_stride,
+      hipLaunchKernelGGL((wyr_w_kernel<4>), gw, dim3(kSumWaves * 64), 0, stream, Ppart, nstrips, nrp, gram_strips, Tsrc, t_stride,
                          ldt, c.k, Wbuf, nx, hi, c.t_trans ? 1 : 0);
       break;
   }
@@ -549,7 +590,7 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
   const dim3 ga((unsigned)nx, (unsigned)nrb, (unsigned)c.batch);
 #define WYR_APPLY_FW(NB_, VEC_, FW_, SEPX_)                                                                        \
   hipLaunchKernelGGL((wyr_apply_kernel<NB_, VEC_, FW_, SEPX_>), ga, dim3(64), 0, stream, c.H, c.hs0, c.ldh, c.n, c.kv, \
-                     c.k, xc_begin, c.c_end, c.rows_per_blk, Wbuf, nx, hi, Ppart, nstrips, nrb, gram_strips, Tsrc,   \
+                     c.k, xc_begin, c.c_end, c.rows_per_blk, Wbuf, nx, hi, Ppart, nstrips, nrp, gram_strips, Tsrc,   \
                      t_stride, ldt, c.X, c.xs0, c.ldx, c.xcols, vcols)
 #define WYR_APPLY(NB_)                                                                                             \
   do {                                                                                                             \
