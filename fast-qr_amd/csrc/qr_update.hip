@@ -464,18 +464,25 @@ __global__ void __launch_bounds__(64) wyr_apply_kernel(float* __restrict__ H, in
 // ---------------------------------------------------------------------------
 // Host side
 // ---------------------------------------------------------------------------
+// Partials stored per launch of nrb row blocks: one per four row blocks from
+// 8 row blocks on (summed in the partial kernel's LDS), else one each.
+static int wyr_partial_groups(int nrb) { return nrb >= 8 ? (nrb + 3) / 4 : nrb; }
+
 int wyr_rows_per_block(int m, int64_t batch, int cols) {
   // enough waves to fill the GPU (about 1024 (strip, row block) pairs per
   // launch) with as few row blocks as possible (each adds a partial to sum)
   const int64_t strips = (cols + 31) / 32;
   int r = 512;
   while (r > 128 && batch * strips * ((m + r - 1) / r) < 1024) r >>= 1;
-  // A batch of a few matrices still under that count at 128 rows: 64-row
-  // blocks (measured on MI355X: 2 x 4096 13.3 -> 12.8 ms; for 8 x 2048 the
-  // longer partial sum of each apply wave outweighs the extra waves).  The
-  // strip bound keeps batch * strips * row blocks within the partial-product
-  // area that wyr_workspace_floats sizes for 128-row blocks.
-  if (batch <= 4 && batch * strips * ((m + 127) / 128) < 1024 && 2 * strips <= m / 64 + 2) r = 64;
+  // A batch of a few matrices still under that count at 128 rows: 32-row
+  // blocks, one tile per wave (measured on MI355X, 2 x 4096: 128-row blocks
+  // 13.3 ms, 64-row 12.9, 32-row with the partials grouped by four 12.2; for
+  // 8 x 2048 smaller blocks gain nothing).  Only where the partials fit the
+  // area wyr_workspace_floats sizes for 128-row blocks at m rows.
+  if (batch <= 4 && batch * strips * ((m + 127) / 128) < 1024) {
+    const int64_t nrp = wyr_partial_groups((m + 31) / 32);
+    if (strips * nrp <= ((int64_t)(m + 31) / 32 + kWyrMaxBlk) * ((m + 127) / 128)) r = 32;
+  }
   return r;
 }
 
@@ -496,8 +503,8 @@ hipError_t launch_wyr(const WyrCall& c, hipStream_t stream) {
   const int nrb = (m + c.rows_per_blk - 1) / c.rows_per_blk;
   // partials per four row blocks once there are 8 or more: W is formed (by
   // every apply wave on the critical path) from a quarter as many
-  const int pg = nrb >= 8 ? 4 : 1;
-  const int nrp = (nrb + pg - 1) / pg;
+  const int nrp = wyr_partial_groups(nrb);
+  const int pg = nrp == nrb ? 1 : 4;
   const int nstrips = (c.c_end - c.c_begin + 31) / 32;
   const int gram_strips = c.gram ? nblk : 0;  // the first strips of [c_begin, c_end) are the group's own columns
   const int gram_end = c.gram ? c.kv + c.k : 0;
