@@ -10,12 +10,14 @@
 //   X <- X - V (T^T (V^T X))      V: m x k (k <= 128 reflectors of up to four
 //                                 consecutive panels), T: k x k, X: m x c
 //
-//   wyr_partial_kernel  grid (32-column strips, row blocks, batch), one wave:
-//                       P_rb = V_rb^T X_rb for its row block (fp32 MFMA
+//   wyr_partial_kernel  grid (32-column strips, row-block groups, batch), one
+//                       wave per row block: P_rb = V_rb^T X_rb (fp32 MFMA
 //                       32x32x2, X tiles as the B operand in accumulator
-//                       layout).  Strips inside the group's own columns are
-//                       read as V (unit diagonal, zeros above), which gives the
-//                       Gram matrix V^T V the group T needs.
+//                       layout); from 8 row blocks on, four per workgroup,
+//                       their partials summed in LDS into one.  Strips inside
+//                       the group's own columns are read as V (unit diagonal,
+//                       zeros above), which gives the Gram matrix V^T V the
+//                       group T needs.
 //   wyr_tg_kernel       one workgroup per matrix: sums the Gram partials and
 //                       joins the panels' T factors into the group T
 //                       (T_[1:j] = [[T_[1:j-1], -T_[1:j-1] G_[1:j-1,j] T_j], [0, T_j]]).
