@@ -132,6 +132,23 @@ def test_repairs_on_ragged_and_tiny_sizes(cuda, batch, n, pw):
         assert np.abs(tau - to).max() <= 1e-4
 
 
+@pytest.mark.parametrize("mode", ["tf32-input", "bf16-input"])
+@pytest.mark.parametrize("batch,n", [(2, 512), (1, 1024)])
+def test_full_repair_at_workload_sizes(cuda, mode, batch, n):
+    """Both repairs at the sizes of the 640 x 512 and 60 x 1024 workloads (a
+    leading sub-batch): the official gates and |R_ii| / tau agreement with CPU
+    geqrf, as for the fp32 path."""
+    _say(f"[mixed repaired, large] mode={mode} batch={batch} n={n}")
+    a = case(batch, n, 1, 900 + n)
+    h, tau = run(a, cuda, panel_width=32, precision_mode=mode, r_maintenance_mode="panel-prefix",
+                 panel_refresh_mode="prefix")
+    ok, msg = checker.official_check(a, h, tau)
+    assert ok, msg
+    h_ref, tau_ref = torch.geqrf(a)
+    rep = checker.rdiag_tau_agreement(a, torch.from_numpy(h), torch.from_numpy(tau), h_ref, tau_ref)
+    assert rep.ok, rep.message()
+
+
 def test_r_maintenance_alone_still_fails(cuda):
     a = case(3, 64, 1, 9)
     h, tau = run(a, cuda, panel_width=16, precision_mode="tf32-input", r_maintenance_mode="panel-prefix")
