@@ -344,3 +344,56 @@ def test_missing_native_library_fails_loudly(monkeypatch, tmp_path):
         _lib.cdll()
     with pytest.raises(fastqr.FastQRUnavailable):
         _lib.ext()
+
+
+def _mixed(lib, A=8, b=2, n=100, H=16, h_s=None, tau=32, pw=32, prec=0, flags=0, ws=64, ws_bytes=1 << 30):
+    h_s0, h_s1, h_s2 = (n * n, 1, n) if h_s is None else h_s
+    base = 1 << 40  # fake, never-dereferenced addresses (validation only)
+    return lib.fastqr_geqrf_mixed_f32(base * A if A else None, b, n, n * n, n, 1, base * H if H else None, h_s0,
+                                      h_s1, h_s2, base * tau if tau else None, n, 1, pw, prec, flags,
+                                      base * ws if ws else None, ws_bytes, None)
+
+
+def test_mixed_entry_validates_without_launching():
+    lib = fastqr.cdll()
+    assert _mixed(lib, b=0) == _lib.FASTQR_OK and _mixed(lib, n=0) == _lib.FASTQR_OK
+    assert _mixed(lib, pw=8) == _lib.FASTQR_EINVAL
+    assert b"panel_width must be 16 or 32" in lib.fastqr_last_error()
+    assert _mixed(lib, prec=7) == _lib.FASTQR_EINVAL
+    assert _mixed(lib, flags=4) == _lib.FASTQR_EINVAL
+    assert b"unknown flags" in lib.fastqr_last_error()
+    assert _mixed(lib, n=3000) == _lib.FASTQR_EINVAL
+    assert _mixed(lib, A=0) == _lib.FASTQR_EINVAL
+    assert _mixed(lib, h_s=(20000, 100, 1)) == _lib.FASTQR_ELAYOUT
+    assert _mixed(lib, A=16) == _lib.FASTQR_EOVERLAP  # the repairs read A again: no overlap at all
+    assert b"A and H overlap" in lib.fastqr_last_error()
+    assert _mixed(lib, ws_bytes=64) == _lib.FASTQR_EWORKSPACE
+    assert _mixed(lib, ws=0) == _lib.FASTQR_EWORKSPACE
+    lib.fastqr_debug_force_error(-99)
+    assert _mixed(lib) == -99
+
+
+def test_mixed_workspace_bytes():
+    lib = fastqr.cdll()
+    plain = lib.fastqr_geqrf_mixed_workspace_bytes(2, 100, 32, 0)
+    refresh = lib.fastqr_geqrf_mixed_workspace_bytes(2, 100, 32, _lib.FASTQR_MIXED_PANEL_REFRESH)
+    both = lib.fastqr_geqrf_mixed_workspace_bytes(2, 100, 32, 3)
+    assert plain >= 2 * 12 * 32 * 32 * 4 and plain % 256 == 0
+    assert plain < refresh < both
+    assert both >= plain + 2 * 100 * 100 * 4  # R maintenance holds a copy of the batch
+    for bad in ((0, 100, 32, 0), (2, 0, 32, 0), (2, 100, 8, 0), (2, 100, 32, 4), (2, 4096, 32, 0)):
+        assert lib.fastqr_geqrf_mixed_workspace_bytes(*bad) == 0
+
+
+def test_mixed_wrapper_rejects_bad_arguments_before_any_device_work():
+    a = torch.zeros((1, 8, 8))
+    for kw, text in [(dict(panel_width=0), "panel_width must be positive"),
+                     (dict(panel_width=24), "panel_width must be one of"),
+                     (dict(update_mode="reflectors"), "update_mode must be one of"),
+                     (dict(precision_mode="fp8"), "precision_mode must be one of"),
+                     (dict(r_maintenance_mode="x"), "r_maintenance_mode must be one of"),
+                     (dict(panel_refresh_mode="x"), "panel_refresh_mode must be one of")]:
+        with pytest.raises(ValueError, match=text):
+            fastqr.blocked_geqrf_mixed(a, **kw)
+    with pytest.raises(ValueError, match="CUDA"):
+        fastqr.blocked_geqrf_mixed(a)  # a CPU tensor: no fallback
